@@ -1,0 +1,129 @@
+/*
+ * tilert_amd -- C ABI of the MI355X (gfx950) FP8 decode hot path.
+ *
+ * A plain C interface: device pointers, sizes and a hipStream_t passed as void*.
+ * No torch types.  Every function is destination-passing (the caller owns every
+ * output and workspace; the library never allocates) and returns an int status:
+ *   0 = ok, 1 = bad argument, 2 = HIP launch error, 3 = unsupported shape/option;
+ * on failure tl_last_error() returns a thread-local message.  Kernels are enqueued on
+ * the given stream and never synchronise it.
+ *
+ * Conventions: fp8 = OCP float8_e4m3fn bytes; bf16 = uint16 bit patterns; block size
+ * 128; activation scales fp32 [rows, K/128]; weight scales fp32 [ceil(N/128), K/128],
+ * row-major weights [N, K].
+ *
+ * Reference interfaces replaced (paths relative to the tile-ai/TileRT tree):
+ *   tl_act_quant        act_quant            tilert/models/deepseek_v3_2/refs/kernel.py:252-279
+ *                       (fused form: rmsnorm_quant_op  .../ops/rmsnorm_quant.py:25-35)
+ *   tl_weight_dequant   weight_dequant       .../refs/kernel.py:97-129
+ *   tl_fp8_gemm         fp8_gemm             .../refs/kernel.py:282-306; the FP8 GEMVs behind
+ *                       projx_wqkva_op (.../ops/projx_wqkva.py:22-48), rmsnorm_proj_qb_op,
+ *                       unproj_o_allreduce_op, rmsnorm_up_gate_silu_op, down_allreduce_op
+ *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
+ *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
+ *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
+ *   tl_topk_rows           topk_accurate_op               .../ops/topk.py:62-109
+ *   (sparse_index_topk_dsv32_op, .../ops/sparse_index.py:72-128, = scores + top-k)
+ */
+#ifndef TILERT_AMD_H_
+#define TILERT_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* scale_mode values for tl_act_quant */
+#define TL_SCALE_REFERENCE 0 /* s = max(amax,1e-4) * fp32(1/448)   refs/kernel.py:191 */
+#define TL_SCALE_UE8M0 1     /* s = 2^ceil(log2(max(amax,1e-4)/448)) refs/kernel.py:140-151 */
+#define TL_SCALE_DIV 2       /* s = max(amax,1e-4) / 448 (IEEE division) */
+
+const char* tl_last_error(void);
+const char* tl_version(void);
+
+/* Per-(row, 128-column group) quantisation of bf16 x [rows, K] to e4m3fn y [rows, K] with
+ * fp32 scales s [rows, K/128]: y = e4m3(clamp(x / s, -448, 448)), RNE, IEEE division.
+ * group must be 128.  Replaces act_quant (refs/kernel.py:252-279). */
+int tl_act_quant(const void* x_bf16, void* y_fp8, float* s, int64_t rows, int64_t K,
+                 int64_t group, int scale_mode, void* stream);
+
+/* 128x128 block quantisation of a weight w [N, K] (fp32, or bf16 when w_is_bf16):
+ * s = block_amax / 448 (1 for an all-zero block), q = e4m3(clamp(w / s)).  Weight
+ * preparation (the per-op converters' job in the reference, e.g. convert_to_mma in
+ * expert_sel_up_gate_silu.py); not on the per-token path. */
+int tl_weight_quant(const void* w, int w_is_bf16, void* q_fp8, float* s, int64_t N, int64_t K,
+                    void* stream);
+
+/* out[n,k] = fp32(q[n,k]) * s[n/128, k/128], written as fp32 or bf16 (out_bf16 = 1).
+ * Replaces weight_dequant / _weight_dequant_torch (refs/kernel.py:82-129). */
+int tl_weight_dequant(const void* q_fp8, const float* s, void* out, int out_bf16, int64_t N,
+                      int64_t K, void* stream);
+
+/* c[M,N] bf16 = (a . b^T) with per-128-K-block scaling, fp32 accumulation.
+ * a fp8 [M,K], a_s fp32 [M,K/128], b fp8 [N,K], b_s fp32 [ceil(N/128),K/128].
+ * Requires K % 128 == 0, N % 16 == 0, 1 <= M <= 256, 16-byte aligned a and b.
+ * Narrow problems split K across workgroups and need a workspace of
+ * tl_fp8_gemm_workspace_bytes(M,N,K) bytes, ZERO-FILLED before its first use; the kernel
+ * leaves it ready for the next call.  Calls that share a workspace must be ordered
+ * (same stream).  Replaces fp8_gemm (refs/kernel.py:282-306). */
+size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s, void* c_bf16,
+                int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/* MoE gate/up + SwiGLU at one expert-parallel shard.
+ * x fp8 [M, D] + x_s fp32 [M, D/128] (act_quant of the hidden state); per local expert e
+ * (0 <= e < n_local) gate G_e and up U_e: fp8 [I, D] at gate + e*I*D, scales
+ * [I/128, D/128] at gate_s + e*(I/128)*(D/128) (same for up).  topk_idx int32 [M, topk]
+ * holds global expert ids; the shard owns ids [expert_begin, expert_begin + n_local).
+ * Every local expert hit by at least one token gets a slot (slots in ascending expert
+ * order); h bf16 [n_local, M, I] receives, for slot s and EVERY token t,
+ * h[s,t,:] = bf16(silu(x_t . G^T) * (x_t . U^T)) (rows of unrouted tokens are computed
+ * but ignored by tl_moe_down_combine).  M <= 16, D and I multiples of 128.
+ * Replaces the grouped GEMM of expert_select_up_gate_silu_op
+ * (expert_sel_up_gate_silu.py:23-48, golden :670-692); routing itself is an input. */
+int tl_moe_gate_up_swiglu(const void* x_fp8, const float* x_s, const void* gate,
+                          const float* gate_s, const void* up, const float* up_s,
+                          const int32_t* topk_idx, int64_t M, int64_t topk, int64_t expert_begin,
+                          int64_t n_local, int64_t D, int64_t I, void* h_bf16, void* stream);
+
+/* MoE down projection + routing-weighted combine.
+ * h bf16 [n_local, M, I] from tl_moe_gate_up_swiglu (act-quantised per 1x128 inside,
+ * scale_mode as tl_act_quant); per local expert down D_e fp8 [D, I] at down + e*D*I,
+ * scales [D/128, I/128]; topk_w fp32 [M, topk].
+ * y[t] = bf16( sum_e bf16(w[t,e] * (hq[t,e] . D_e^T)) ), experts summed in ascending
+ * order, 0 for tokens with no local expert.  Replaces expert_down_allreduce_op
+ * (expert_down_allreduce.py:23-63, golden :455-468) at one shard (no allreduce). */
+int tl_moe_down_combine(const void* h_bf16, const void* down, const float* down_s,
+                        const int32_t* topk_idx, const float* topk_w, int64_t M, int64_t topk,
+                        int64_t expert_begin, int64_t n_local, int64_t D, int64_t I,
+                        int scale_mode, void* y_bf16, void* stream);
+
+/* DSA lightning-indexer scores over an fp8 key cache.
+ * q fp8 [M, H, 128]; q_s fp32 per token [M] (q_s_per_head = 0) or per (token, head)
+ * [M, H] (q_s_per_head = 1); k fp8 [L, 128]; k_s fp32 [L]; w bf16 [M, H].
+ * logits fp32 [M, ld] (ld >= L): logits[t,l] = sum_h w[t,h]*ReLU(qd[t,h].kd[l]) for
+ * l <= cur_pos + t, -inf for cur_pos + t < l < L.  H in {32, 64}, M*H <= 256.
+ * Replaces sparse_index_op (ops/sparse_index.py:11-69) for an fp8 cache. */
+int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
+                          const void* k_fp8, const float* k_s, const void* w_bf16,
+                          float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
+                          int64_t cur_pos, void* stream);
+
+/* Exact per-row top-k.  logits fp32 [rows, ld]; row i considers columns
+ * [0, valid_base + 1 + i) (capped at ld) -- topk_accurate's convention with
+ * valid_base = seq_len - num_samples (ops/topk.py:77-80,101).  out int32 [rows, k]:
+ * indices in descending score order (ties: ascending index), -1 past the valid length.
+ * workspace of tl_topk_workspace_bytes(rows, ld, k) bytes (no initialisation needed).
+ * Replaces topk_accurate_op (ops/topk.py:62-109). */
+size_t tl_topk_workspace_bytes(int64_t rows, int64_t ld, int64_t k);
+int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64_t valid_base, int64_t k,
+                 int32_t* out, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILERT_AMD_H_ */

@@ -1,0 +1,256 @@
+"""torch-CPU restatement of the reference goldens for the FP8 decode hot path.
+
+Test infrastructure only (see ``oracle/__init__.py``).  All citations are relative to the
+reference tree (tile-ai/TileRT).  Tensors are CPU tensors; fp8 data is carried as
+``torch.float8_e4m3fn`` (or uint8 codes where noted).
+
+Conventions shared with the HIP library:
+  * block size 128 everywhere (``tilert/models/deepseek_config.py`` ``block_size = 128``);
+  * activation scales are one fp32 per (row, 128-column group);
+  * weight scales are one fp32 per (128-row, 128-column) block, shape
+    [ceil(N/128), ceil(K/128)];
+  * outputs of linears are bf16 (``torch.get_default_dtype()`` in DeepSeek inference).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+BLOCK = 128
+E4M3_MAX = 448.0
+# tilelang folds ``1 / fp8_max`` into an fp32 immediate (refs/kernel.py:160)
+INV_448_F32 = torch.tensor(1.0 / 448.0, dtype=torch.float32)
+AMAX_FLOOR_F32 = torch.tensor(1e-4, dtype=torch.float32)
+
+SCALE_MODE_REFERENCE = 0  # s = amax * fp32(1/448)             refs/kernel.py:191
+SCALE_MODE_UE8M0 = 1  # s = 2^ceil(log2(amax * fp32(1/448)))  refs/kernel.py:140-151,189
+SCALE_MODE_DIV = 2  # s = amax / 448 (IEEE division), the BASELINE statement
+
+
+def _group_scale(amax: torch.Tensor, scale_mode: int) -> torch.Tensor:
+    """Per-group scale from the fp32 amax (refs/kernel.py:186-191)."""
+    amax = torch.maximum(amax, AMAX_FLOOR_F32)
+    if scale_mode == SCALE_MODE_REFERENCE:
+        return amax * INV_448_F32
+    if scale_mode == SCALE_MODE_DIV:
+        return amax / torch.tensor(448.0, dtype=torch.float32)
+    if scale_mode == SCALE_MODE_UE8M0:
+        # _fast_round_scale: pow2(ceil(log2(amax * inv))) with exponent/mantissa bit ops
+        v = (amax * INV_448_F32).contiguous()
+        bits = v.view(torch.int32).to(torch.int64)
+        exp = (bits >> 23) & 0xFF
+        man = bits & ((1 << 23) - 1)
+        e = exp - 127 + (man != 0).to(torch.int64)
+        return ((e + 127) << 23).to(torch.int32).view(torch.float32)
+    raise ValueError(f"unknown scale_mode {scale_mode}")
+
+
+def act_quant(
+    x: torch.Tensor, block_size: int = BLOCK, scale_mode: int = SCALE_MODE_REFERENCE
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-(row, 128-group) e4m3fn quantisation.
+
+    Follows ``act_quant_kernel`` (refs/kernel.py:154-199) and its wrapper ``act_quant``
+    (refs/kernel.py:252-279): amax over the group in fp32, floored at 1e-4, scale per
+    ``scale_mode``, then ``e4m3fn(clamp(x / s, -448, 448))`` with IEEE fp32 division and
+    round-to-nearest-even.  Returns (y float8_e4m3fn, s float32 [..., K/128]).
+    """
+    assert x.shape[-1] % block_size == 0
+    K = x.shape[-1]
+    xf = x.float().reshape(-1, K // block_size, block_size)
+    amax = xf.abs().amax(dim=-1)
+    s = _group_scale(amax, scale_mode)
+    y = torch.clamp(xf / s[..., None], -E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    return y.reshape(x.shape), s.reshape(*x.shape[:-1], K // block_size)
+
+
+def act_dequant(y: torch.Tensor, s: torch.Tensor, block_size: int = BLOCK) -> torch.Tensor:
+    """fp32 x = fp8 * group scale, as the goldens do (projx_wqkva.py:280-285)."""
+    K = y.shape[-1]
+    yf = y.float().reshape(-1, K // block_size, block_size)
+    return (yf * s.reshape(-1, K // block_size, 1)).reshape(y.shape)
+
+
+def weight_quant(w: torch.Tensor, block_size: int = BLOCK) -> tuple[torch.Tensor, torch.Tensor]:
+    """128x128 block quantisation of a weight (synthetic-weight preparation).
+
+    BASELINE convention: ``s = block_amax / 448`` (IEEE division), ``q = e4m3fn(w / s)``.
+    Rows/columns that do not fill a block (e.g. N=576) form a partial block.  All-zero
+    blocks get s = 1 (so that dequantisation returns exact zeros).
+    """
+    N, K = w.shape
+    nb, kb = math.ceil(N / block_size), math.ceil(K / block_size)
+    wp = torch.zeros(nb * block_size, kb * block_size, dtype=torch.float32)
+    wp[:N, :K] = w.float()
+    blocks = wp.reshape(nb, block_size, kb, block_size)
+    amax = blocks.abs().amax(dim=(1, 3))
+    s = torch.where(amax > 0, amax / torch.tensor(448.0), torch.ones_like(amax))
+    q = torch.clamp(blocks / s[:, None, :, None], -E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+    q = q.reshape(nb * block_size, kb * block_size)[:N, :K].contiguous()
+    return q, s.contiguous()
+
+
+def weight_dequant(q: torch.Tensor, s: torch.Tensor, block_size: int = BLOCK) -> torch.Tensor:
+    """fp32 ``W[n,k] = fp32(Wq[n,k]) * S[n//128, k//128]``.
+
+    ``_weight_dequant_torch`` (refs/kernel.py:82-94), extended to partial edge blocks.
+    """
+    N, K = q.shape
+    s_full = s.repeat_interleave(block_size, 0)[:N].repeat_interleave(block_size, 1)[:, :K]
+    return q.float() * s_full
+
+
+def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor) -> torch.Tensor:
+    """``C = dequant(A) . dequant(B)^T`` in fp32, output bf16.
+
+    The golden of every FP8 projection (projx_wqkva.py:280-294: dequantise x per 1x128,
+    matmul with the fp32 dequantised weight, ``.to(torch.bfloat16)``), which is what
+    ``fp8_gemm`` (refs/kernel.py:282-306) computes with per-128-K-block scaling.
+    """
+    K = a.shape[-1]
+    xa = act_dequant(a.reshape(-1, K), a_s.reshape(-1, K // BLOCK))
+    wb = weight_dequant(b, b_s)
+    c = xa @ wb.T
+    return c.to(torch.bfloat16).reshape(*a.shape[:-1], b.shape[0])
+
+
+def linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, scale_mode: int = 0) -> torch.Tensor:
+    """``common.linear`` FP8 branch (tilert/models/common.py:83-89): act_quant -> fp8_gemm."""
+    xq, xs = act_quant(x, BLOCK, scale_mode)
+    return fp8_gemm(xq, xs, wq, ws)
+
+
+def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+    """``silu(g) * u`` in fp32 (expert_sel_up_gate_silu.py:687)."""
+    return F.silu(g.float()) * u.float()
+
+
+def local_pairs(topk_idx: torch.Tensor, expert_begin: int, n_local: int) -> list[tuple[int, int, int]]:
+    """(token, k-slot, local expert) for every routed pair that lands on this shard."""
+    out = []
+    M, topk = topk_idx.shape
+    for t in range(M):
+        for j in range(topk):
+            e = int(topk_idx[t, j]) - expert_begin
+            if 0 <= e < n_local:
+                out.append((t, j, e))
+    return out
+
+
+def hit_experts(topk_idx: torch.Tensor, expert_begin: int, n_local: int) -> list[int]:
+    """Local experts hit by at least one token, ascending (the slot order)."""
+    return sorted({e for (_, _, e) in local_pairs(topk_idx, expert_begin, n_local)})
+
+
+def moe_gate_up(
+    x: torch.Tensor,
+    gq: torch.Tensor, gs: torch.Tensor, uq: torch.Tensor, us: torch.Tensor,
+    topk_idx: torch.Tensor, expert_begin: int, scale_mode: int = 0,
+) -> tuple[torch.Tensor, list[int]]:
+    """Grouped gate/up + SwiGLU for every hit local expert and every token.
+
+    Per (token, expert): ``h = bf16(silu(x.G^T) * (x.U^T))`` with fp32 products -- the
+    per-expert loop of ``ExpertSelectUpGateSiLU.golden_forward``
+    (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:670-692), at the W8A8 precision of
+    BASELINE config 2 (x act-quantised per 1x128, weights 128x128 block-scaled).
+    Returns h [n_hit, M, I] bf16 (slot order = ascending local expert id) and the hit list.
+    """
+    E = gq.shape[0]
+    xq, xs = act_quant(x, BLOCK, scale_mode)
+    xd = act_dequant(xq, xs)
+    hits = hit_experts(topk_idx, expert_begin, E)
+    hs = []
+    for e in hits:
+        g = xd @ weight_dequant(gq[e], gs[e]).T
+        u = xd @ weight_dequant(uq[e], us[e]).T
+        hs.append(swiglu(g, u).to(torch.bfloat16))
+    I = gq.shape[1]
+    h = torch.stack(hs) if hs else torch.zeros(0, x.shape[0], I, dtype=torch.bfloat16)
+    return h, hits
+
+
+def moe_down(
+    h: torch.Tensor, hits: list[int],
+    dq: torch.Tensor, ds: torch.Tensor,
+    topk_idx: torch.Tensor, topk_w: torch.Tensor, expert_begin: int, scale_mode: int = 0,
+) -> torch.Tensor:
+    """Down projection + routing-weighted sum over the local experts.
+
+    ``y[t] = bf16( sum_e bf16(w[t,e] * (h[t,e] . D_e^T)) )`` -- the order of
+    ``ExpertDownAllReduce.golden_forward`` (deepseek_v3_2/ops/expert_down_allreduce.py:455-468:
+    each weighted expert term cast to bf16, then summed), with h act-quantised per 1x128
+    for the FP8 down GEMM.  Terms are summed in fp32 in ascending expert order.
+    """
+    M = topk_idx.shape[0]
+    D = dq.shape[1]
+    acc = torch.zeros(M, D, dtype=torch.float32)
+    pairs = local_pairs(topk_idx, expert_begin, dq.shape[0])
+    slot = {e: i for i, e in enumerate(hits)}
+    wd = {e: weight_dequant(dq[e], ds[e]) for e in hits}
+    for e in hits:
+        for (t, j, ee) in pairs:
+            if ee != e:
+                continue
+            hq, hsc = act_quant(h[slot[e], t][None], BLOCK, scale_mode)
+            term = act_dequant(hq, hsc)[0] @ wd[e].T
+            acc[t] += (term * topk_w[t, j].float()).to(torch.bfloat16).float()
+    return acc.to(torch.bfloat16)
+
+
+def moe_forward(x, gq, gs, uq, us, dq, ds, topk_idx, topk_w, expert_begin, scale_mode=0):
+    """Whole local-expert MoE layer (config 2): gate/up + SwiGLU, down, weighted sum."""
+    h, hits = moe_gate_up(x, gq, gs, uq, us, topk_idx, expert_begin, scale_mode)
+    return moe_down(h, hits, dq, ds, topk_idx, topk_w, expert_begin, scale_mode)
+
+
+def indexer_scores(
+    q: torch.Tensor, q_s: torch.Tensor, k: torch.Tensor, k_s: torch.Tensor,
+    w: torch.Tensor, cur_pos: int,
+) -> torch.Tensor:
+    """DSA lightning-indexer logits, fp32 [M, L].
+
+    ``score[t,l] = sum_h w[t,h] * ReLU(q[t,h] . k[l])`` on dequantised fp8 inputs
+    (q: [M,H,128] e4m3fn with scale per token [M] or per (token, head) [M,H];
+    k: [L,128] e4m3fn with per-key scale [L]; w: bf16 [M,H]).  Token t sits at position
+    ``cur_pos + t`` and sees keys ``l <= cur_pos + t``; masked positions are -inf.
+    The reference ships no golden for this (ops/sparse_index.py:11-69 describes it as
+    "q * kv * weights"); the formula is the one BASELINE config 4 states.
+    """
+    M, H, Dh = q.shape
+    L = k.shape[0]
+    qs = q_s.float().reshape(M, -1)
+    qd = q.float() * (qs[:, :, None] if qs.shape[1] == H else qs[:, :1, None])
+    kd = k.float() * k_s.float().reshape(L, 1)
+    logits = torch.einsum("thd,ld->thl", qd, kd)
+    logits = torch.relu(logits)
+    score = torch.einsum("thl,th->tl", logits, w.float())
+    pos = torch.arange(L)[None, :]
+    lim = (cur_pos + torch.arange(M))[:, None]
+    return torch.where(pos <= lim, score, torch.tensor(float("-inf")))
+
+
+def topk_rows(logits: torch.Tensor, valid: list[int], k: int) -> torch.Tensor:
+    """Per-row top-k indices among the first ``valid[i]`` columns, int32 [rows, k].
+
+    ``TopK.golden_forward`` is ``logits.topk(min(k, L))[1]`` (ops/topk.py:128-143); sample i
+    of ``topk_accurate`` only considers its valid prefix (ops/topk.py:77-80,101).  Order:
+    descending score, ties by ascending index; slots beyond the valid length are -1.
+    """
+    rows = logits.shape[0]
+    out = torch.full((rows, k), -1, dtype=torch.int32)
+    for i in range(rows):
+        v = logits[i, : valid[i]].double()
+        n = min(k, v.numel())
+        if n == 0:
+            continue
+        order = sorted(range(v.numel()), key=lambda j: (-float(v[j]), j)) if v.numel() < 4096 \
+            else _sort_desc_stable(v)
+        out[i, :n] = torch.tensor(order[:n], dtype=torch.int32)
+    return out
+
+
+def _sort_desc_stable(v: torch.Tensor) -> list[int]:
+    # stable sort on -v keeps ascending index among equal scores
+    return torch.sort(-v, stable=True).indices.tolist()

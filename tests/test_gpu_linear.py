@@ -1,0 +1,117 @@
+"""GPU parity of act_quant, weight_quant/dequant and the block-scaled FP8 GEMM against
+the CPU oracle (bit-exact for quantisation, stated tolerances for GEMM outputs)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference as ref
+from tests._tol import assert_gemm_close
+from tilert_amd import kernel as K
+from tilert_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _all_bf16_finite() -> torch.Tensor:
+    bits = np.arange(65536, dtype=np.uint32)
+    f = (bits << 16).view(np.float32)
+    f = f[np.isfinite(f)]
+    pad = (-len(f)) % 128
+    f = np.concatenate([f, np.zeros(pad, np.float32)])
+    return torch.from_numpy(f).to(torch.bfloat16).reshape(-1, 128)
+
+
+@pytest.mark.parametrize("mode,fmt", [(0, None), (1, "ue8m0"), (2, "div")])
+def test_act_quant_exhaustive_bf16(cuda, mode, fmt):
+    """Every finite bf16 value, in groups mixing magnitudes (shuffled) and in sorted
+    groups (so both tiny and huge amax occur): codes and scales bit-exact."""
+    x = _all_bf16_finite()
+    g = torch.Generator().manual_seed(0)
+    xs = x.flatten()[torch.randperm(x.numel(), generator=g)].reshape(-1, 128)
+    for xx in (x, xs, torch.cat([x, xs], 1)):
+        y, s = K.act_quant(xx.to(cuda).contiguous(), 128, fmt)
+        ry, rs = ref.act_quant(xx, 128, mode)
+        assert torch.equal(s.cpu(), rs), "scales differ"
+        assert torch.equal(y.cpu().view(torch.uint8), ry.view(torch.uint8)), "codes differ"
+
+
+def test_act_quant_edge_groups(cuda):
+    x = torch.zeros(4, 256, dtype=torch.bfloat16)
+    x[1, :128] = 3.0
+    x[2, 5] = -1e-30
+    x[3, 130] = 448.0
+    y, s = K.act_quant(x.to(cuda), 128)
+    ry, rs = ref.act_quant(x, 128)
+    assert torch.equal(s.cpu(), rs)
+    assert torch.equal(y.cpu().view(torch.uint8), ry.view(torch.uint8))
+
+
+@pytest.mark.parametrize("N,Kd", [(128, 128), (576, 7168), (300, 520), (2048, 1536)])
+def test_weight_quant_bit_exact(cuda, N, Kd):
+    w = synth.weight_fp32(N, Kd, synth.gen(N + Kd))
+    q, s = K.weight_quant(w.to(cuda))
+    rq, rs = ref.weight_quant(w)
+    assert torch.equal(s.cpu(), rs)
+    assert torch.equal(q.cpu().view(torch.uint8), rq.view(torch.uint8))
+    d = K.weight_dequant(q, s)
+    assert torch.equal(d.cpu(), ref.weight_dequant(rq, rs).to(torch.get_default_dtype()))
+
+
+GEMM_CASES = [
+    # (M, N, K)
+    (1, 256, 512),
+    (4, 576, 7168),     # wkv_a: split-K + partial last scale row
+    (4, 3072, 1536),    # wq_b
+    (4, 4096, 512),     # wkv_b
+    (4, 7168, 2048),    # wo
+    (3, 1536, 7168),    # wq_a, odd M
+    (16, 2048, 1024),
+    (17, 512, 1024),
+    (64, 1024, 2048),
+    (256, 512, 1024),
+]
+
+
+@pytest.mark.parametrize("M,N,Kd", GEMM_CASES)
+def test_fp8_gemm_vs_oracle(cuda, M, N, Kd):
+    g = synth.gen(1000 + M + N + Kd)
+    x = synth.activations(M, Kd, g)
+    w = synth.weight_fp32(N, Kd, g)
+    wq, ws = ref.weight_quant(w)
+    xq, xs = ref.act_quant(x)
+    out = K.fp8_gemm(xq.to(cuda), xs.to(cuda), wq.to(cuda), ws.to(cuda))
+    out2 = K.fp8_gemm(xq.to(cuda), xs.to(cuda), wq.to(cuda), ws.to(cuda))
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "fp8_gemm is not deterministic"
+    assert_gemm_close(out, ref.fp8_gemm(xq, xs, wq, ws), f"M={M} N={N} K={Kd}")
+
+
+def test_fp8_gemm_one_hot_picks_column(cuda):
+    """x = e_k (one nonzero) selects dequantised column k of W exactly (up to bf16)."""
+    N, Kd = 256, 1024
+    w = synth.weight_fp32(N, Kd, synth.gen(7))
+    wq, ws = ref.weight_quant(w)
+    x = torch.zeros(2, Kd, dtype=torch.bfloat16)
+    x[0, 300] = 1.0
+    x[1, 1023] = -2.0
+    xq, xs = ref.act_quant(x)
+    out = K.fp8_gemm(xq.to(cuda), xs.to(cuda), wq.to(cuda), ws.to(cuda)).cpu()
+    wd = ref.weight_dequant(wq, ws)
+    assert torch.equal(out[0], wd[:, 300].to(torch.bfloat16))
+    assert torch.equal(out[1], (-2.0 * wd[:, 1023]).to(torch.bfloat16))
+
+
+def test_linear_matches_oracle(cuda):
+    from tilert_amd.common import linear
+    M, N, Kd = 4, 1024, 7168
+    g = synth.gen(11)
+    x = synth.activations(M, Kd, g)
+    wq, ws = ref.weight_quant(synth.weight_fp32(N, Kd, g))
+    out = linear(x.to(cuda), wq.to(cuda), ws.to(cuda))
+    assert_gemm_close(out, ref.linear(x, wq, ws), "linear")
+
+
+def test_fp8_gemm_rejects_bad_shapes(cuda):
+    a = torch.zeros(4, 100, dtype=torch.float8_e4m3fn, device=cuda)
+    with pytest.raises((AssertionError, ValueError, RuntimeError)):
+        K.fp8_gemm(a, torch.zeros(4, 1, device=cuda), a, torch.zeros(1, 1, device=cuda))

@@ -1,0 +1,106 @@
+// Shared device helpers for the gfx950 FP8 decode kernels.
+//
+// Conventions (all kernels):
+//   * fp8 is OCP e4m3fn (bias 7, max 448, NaN 0x7f/0xff) -- gfx950's native FP8 format,
+//     used directly by v_mfma_*_f8f6f4 with cbsz/blgp = 0.  No fnuz conversion anywhere.
+//   * block size 128: activation scales per (row, 128 columns), weight scales per
+//     (128 rows, 128 columns), stored row-major [ceil(N/128), K/128].
+//   * bf16 is carried as uint16_t bit patterns; fp32 -> bf16 is round-to-nearest-even.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tl {
+
+constexpr int kBlock = 128;
+constexpr float kE4m3Max = 448.0f;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- error reporting
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+enum Status { kOk = 0, kErrArg = 1, kErrHip = 2, kErrUnsupported = 3 };
+
+// ---------------------------------------------------------------- scalar codecs
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest, ties to even
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// e4m3fn encode, round-to-nearest-even.  Callers clamp to [-448, 448] first (the
+// reference does, refs/kernel.py:193), so the result is always finite.
+__device__ inline uint32_t f32_to_e4m3(float v) {
+  uint32_t u = __float_as_uint(v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  float a = __builtin_fabsf(v);
+  if (a != a) return 0x7fu | sign;
+  uint32_t code;
+  if (a < 0.015625f) {  // below 2^-6: subnormal grid m * 2^-9, m in [0, 8]
+    code = static_cast<uint32_t>(__builtin_rintf(a * 512.0f));  // exact scaling, RNE
+  } else {
+    uint32_t au = __float_as_uint(a);
+    uint32_t e = (au >> 23) - 127u + 7u;  // biased e4m3 exponent, 1..15
+    uint32_t m = au & 0x7fffffu;
+    uint32_t r = (m + 0x7ffffu + ((m >> 20) & 1u)) >> 20;  // RNE to 3 mantissa bits (0..8)
+    code = (e << 3) + r;  // r == 8 carries into the exponent
+    if (code > 0x7eu) code = 0x7eu;  // only reachable for |v| > 448 (clamped by callers)
+  }
+  return code | sign;
+}
+
+// --------------------------------------------------------------- MFMA tile helper
+// One wave: C[16x16] = A[16x128] * B[128x16] in fp8 with fp32 accumulation.
+//
+// Lane l holds A row (l & 15) and B column (l & 15); both operands carry the same
+// 32 K-positions per lane (loaded by the same addressing), so the product sums every
+// K position exactly once whatever the hardware's in-register K order is.  The result
+// layout is the CDNA 16x16 accumulator layout: lane l holds C[4*(l>>4) + j][l & 15].
+__device__ inline v4f mfma_16x16x128_fp8(const v8i& a, const v8i& b) {
+  v4f z = {0.f, 0.f, 0.f, 0.f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 0, 0, 0);
+}
+
+// Byte offsets (within a 128-byte K block) of the two 16-byte pieces lane group g owns.
+__device__ inline int kpiece0(int g) { return g * 16; }
+__device__ inline int kpiece1(int g) { return 64 + g * 16; }
+
+__device__ inline v8i load_kblock(const uint8_t* row_kblock, int g) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(row_kblock + kpiece0(g));
+  const uint4 hi = *reinterpret_cast<const uint4*>(row_kblock + kpiece1(g));
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+// Non-temporal variant for weights that are streamed exactly once.
+__device__ inline v8i load_kblock_stream(const uint8_t* row_kblock, int g) {
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+  const u4 lo = __builtin_nontemporal_load(reinterpret_cast<const u4*>(row_kblock + kpiece0(g)));
+  const u4 hi = __builtin_nontemporal_load(reinterpret_cast<const u4*>(row_kblock + kpiece1(g)));
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+__device__ inline v8i zero_v8i() {
+  v8i r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = 0;
+  return r;
+}
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tl

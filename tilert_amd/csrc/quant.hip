@@ -1,0 +1,157 @@
+// act_quant (per 1x128 group, e4m3fn + fp32 scale), 128x128 block weight quantisation
+// and weight dequantisation.
+#include "common.h"
+#include "../../include/tilert_amd.h"
+
+namespace tl {
+
+// Group scale from the fp32 amax; mirrors refs/kernel.py:186-191 and :140-151.
+__device__ inline float group_scale(float amax, int scale_mode) {
+  amax = fmaxf(amax, 1e-4f);
+  if (scale_mode == TL_SCALE_UE8M0) {
+    uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
+    int e = static_cast<int>((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0 ? 1 : 0);
+    return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+  }
+  if (scale_mode == TL_SCALE_DIV) return amax / 448.0f;
+  return amax * (1.0f / 448.0f);
+}
+
+// One thread = 8 consecutive elements; 16 threads = one 128-element group.
+__global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x,
+                                                        uint8_t* __restrict__ y,
+                                                        float* __restrict__ s, int64_t n_groups,
+                                                        int scale_mode) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t grp = tid >> 4;
+  const bool live = grp < n_groups;
+  uint4 raw = make_uint4(0, 0, 0, 0);
+  if (live) raw = reinterpret_cast<const uint4*>(x)[tid];
+  float v[8];
+  v[0] = bf16_to_f32(raw.x & 0xffff); v[1] = bf16_to_f32(raw.x >> 16);
+  v[2] = bf16_to_f32(raw.y & 0xffff); v[3] = bf16_to_f32(raw.y >> 16);
+  v[4] = bf16_to_f32(raw.z & 0xffff); v[5] = bf16_to_f32(raw.z >> 16);
+  v[6] = bf16_to_f32(raw.w & 0xffff); v[7] = bf16_to_f32(raw.w >> 16);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  const float sc = group_scale(amax, scale_mode);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo |= f32_to_e4m3(fminf(fmaxf(v[i] / sc, -kE4m3Max), kE4m3Max)) << (8 * i);
+    hi |= f32_to_e4m3(fminf(fmaxf(v[i + 4] / sc, -kE4m3Max), kE4m3Max)) << (8 * i);
+  }
+  if (live) {
+    reinterpret_cast<uint2*>(y)[tid] = make_uint2(lo, hi);
+    if ((tid & 15) == 0) s[grp] = sc;
+  }
+}
+
+// One 256-thread workgroup per 128x128 block: amax, s = amax/448 (1 for all-zero
+// blocks), q = e4m3(clamp(w/s)).
+template <typename T>
+__device__ inline float load_w(const T* p);
+template <>
+__device__ inline float load_w<float>(const float* p) { return *p; }
+template <>
+__device__ inline float load_w<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void weight_quant_kernel(const T* __restrict__ w,
+                                                           uint8_t* __restrict__ q,
+                                                           float* __restrict__ s, int64_t N,
+                                                           int64_t K) {
+  __shared__ float red[256];
+  const int64_t nb = blockIdx.y, kb = blockIdx.x;
+  const int64_t KB = cdiv(K, kBlock);
+  const int col = threadIdx.x & 127;
+  const int r0 = threadIdx.x >> 7;  // 0..1
+  const int64_t c = kb * kBlock + col;
+  float amax = 0.f;
+  for (int r = r0; r < kBlock; r += 2) {
+    const int64_t n = nb * kBlock + r;
+    if (n < N && c < K) amax = fmaxf(amax, __builtin_fabsf(load_w(w + n * K + c)));
+  }
+  red[threadIdx.x] = amax;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+    __syncthreads();
+  }
+  amax = red[0];
+  const float sc = amax > 0.f ? amax / 448.0f : 1.0f;
+  if (threadIdx.x == 0) s[nb * KB + kb] = sc;
+  for (int r = r0; r < kBlock; r += 2) {
+    const int64_t n = nb * kBlock + r;
+    if (n < N && c < K) {
+      float v = load_w(w + n * K + c) / sc;
+      q[n * K + c] = static_cast<uint8_t>(f32_to_e4m3(fminf(fmaxf(v, -kE4m3Max), kE4m3Max)));
+    }
+  }
+}
+
+__device__ inline float e4m3_to_f32(uint32_t code) {
+  const uint32_t sign = (code & 0x80u) << 24;
+  const uint32_t e = (code >> 3) & 0xfu, m = code & 7u;
+  float mag;
+  if (e == 0xfu && m == 7u) return __uint_as_float(0x7fc00000u);
+  if (e == 0) mag = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return __uint_as_float(__float_as_uint(mag) | sign);
+}
+
+__global__ __launch_bounds__(256) void weight_dequant_kernel(const uint8_t* __restrict__ q,
+                                                             const float* __restrict__ s,
+                                                             void* __restrict__ out, int64_t N,
+                                                             int64_t K, int out_bf16) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N * K) return;
+  const int64_t n = i / K, k = i - n * K;
+  const float v = e4m3_to_f32(q[i]) * s[(n / kBlock) * cdiv(K, kBlock) + k / kBlock];
+  if (out_bf16) static_cast<uint16_t*>(out)[i] = f32_to_bf16(v);
+  else static_cast<float*>(out)[i] = v;
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+extern "C" int tl_act_quant(const void* x_bf16, void* y_fp8, float* s, int64_t rows, int64_t K,
+                            int64_t group, int scale_mode, void* stream) {
+  if (group != kBlock) { set_error("act_quant: only group size 128 is supported (got %lld)", (long long)group); return kErrUnsupported; }
+  if (rows < 0 || K <= 0 || K % kBlock != 0) { set_error("act_quant: K=%lld must be a positive multiple of 128", (long long)K); return kErrArg; }
+  if (scale_mode < 0 || scale_mode > 2) { set_error("act_quant: bad scale_mode %d", scale_mode); return kErrArg; }
+  if (!x_bf16 || !y_fp8 || !s) { set_error("act_quant: null pointer"); return kErrArg; }
+  if (rows == 0) return kOk;
+  const int64_t n_groups = rows * (K / kBlock);
+  const int64_t threads = n_groups * 16;
+  hipLaunchKernelGGL(act_quant_kernel, dim3(cdiv(threads, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, (uint8_t*)y_fp8, s, n_groups, scale_mode);
+  return check_launch("act_quant");
+}
+
+extern "C" int tl_weight_quant(const void* w, int w_is_bf16, void* q_fp8, float* s, int64_t N,
+                               int64_t K, void* stream) {
+  if (N <= 0 || K <= 0) { set_error("weight_quant: empty weight"); return kErrArg; }
+  if (!w || !q_fp8 || !s) { set_error("weight_quant: null pointer"); return kErrArg; }
+  dim3 grid(cdiv(K, kBlock), cdiv(N, kBlock));
+  if (w_is_bf16)
+    hipLaunchKernelGGL(weight_quant_kernel<uint16_t>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)w, (uint8_t*)q_fp8, s, N, K);
+  else
+    hipLaunchKernelGGL(weight_quant_kernel<float>, grid, dim3(256), 0, (hipStream_t)stream,
+                       (const float*)w, (uint8_t*)q_fp8, s, N, K);
+  return check_launch("weight_quant");
+}
+
+extern "C" int tl_weight_dequant(const void* q_fp8, const float* s, void* out, int out_bf16,
+                                 int64_t N, int64_t K, void* stream) {
+  if (N <= 0 || K <= 0) { set_error("weight_dequant: empty weight"); return kErrArg; }
+  if (!q_fp8 || !s || !out) { set_error("weight_dequant: null pointer"); return kErrArg; }
+  hipLaunchKernelGGL(weight_dequant_kernel, dim3(cdiv(N * K, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)q_fp8, s, out, N, K, out_bf16);
+  return check_launch("weight_dequant");
+}
