@@ -73,6 +73,22 @@ int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s
                 int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                 void* stream);
 
+/* Repack a canonical fp8 weight [N, K] (N % 16 == 0, K % 128 == 0) into MFMA operand
+ * fragments for tl_fp8_gemm_packed: fragment (t, kb) (16 rows x 128 columns) occupies
+ * 2048 contiguous bytes at (t * K/128 + kb) * 2048; within it, byte p*1024 + l*16 + i
+ * (piece p in {0,1}, lane l in [0,64), i in [0,16)) is W[16 t + (l % 16)][128 kb +
+ * 64 p + 16 (l / 16) + i].  packed must hold N*K bytes and not alias b.  Counterpart of
+ * the reference's per-op weight converters (e.g. RMSNormProjQKVAFP8MMAWeightsConverter,
+ * rmsnorm_projx_wqkva.py:18-119): a one-time, load-time layout change. */
+int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* stream);
+
+/* tl_fp8_gemm with b in the fragment-packed layout of tl_fp8_pack_weight (same scales,
+ * same results bit for bit, same workspace rule).  The FP8 GEMV behind the reference's
+ * packed-weight projection ops (projx_wqkva_op, rmsnorm_up_gate_silu_op, ...). */
+int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, const float* b_s,
+                       void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 /* MoE gate/up + SwiGLU at one expert-parallel shard.
  * x fp8 [M, D] + x_s fp32 [M, D/128] (act_quant of the hidden state); per local expert e
  * (0 <= e < n_local) gate G_e and up U_e: fp8 [I, D] at gate + e*I*D, scales

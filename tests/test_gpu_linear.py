@@ -84,6 +84,25 @@ def test_fp8_gemm_vs_oracle(cuda, M, N, Kd):
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "fp8_gemm is not deterministic"
     assert_gemm_close(out, ref.fp8_gemm(xq, xs, wq, ws), f"M={M} N={N} K={Kd}")
+    packed = K.pack_weight(wq.to(cuda), ws.to(cuda))
+    outp = K.fp8_gemm(xq.to(cuda), xs.to(cuda), packed)
+    assert torch.equal(outp, out), "packed-weight GEMM differs from the canonical one"
+
+
+def test_pack_weight_layout(cuda):
+    """The fragment layout documented in include/tilert_amd.h, checked byte by byte."""
+    N, Kd = 48, 384
+    w = torch.randint(0, 256, (N, Kd), dtype=torch.uint8)
+    p = K.pack_weight(w.view(torch.float8_e4m3fn).to(cuda), torch.ones(1, 3, device=cuda)).data.cpu()
+    KB = Kd // 128
+    for t in range(N // 16):
+        for kb in range(KB):
+            frag = p[(t * KB + kb) * 2048:(t * KB + kb + 1) * 2048].reshape(2, 64, 16)
+            for piece in range(2):
+                for lane in range(64):
+                    row = 16 * t + lane % 16
+                    col = 128 * kb + 64 * piece + 16 * (lane // 16)
+                    assert torch.equal(frag[piece, lane], w[row, col:col + 16])
 
 
 def test_fp8_gemm_one_hot_picks_column(cuda):
@@ -115,3 +134,19 @@ def test_fp8_gemm_rejects_bad_shapes(cuda):
     a = torch.zeros(4, 100, dtype=torch.float8_e4m3fn, device=cuda)
     with pytest.raises((AssertionError, ValueError, RuntimeError)):
         K.fp8_gemm(a, torch.zeros(4, 1, device=cuda), a, torch.zeros(1, 1, device=cuda))
+
+
+@pytest.mark.parametrize("M,N,Kd", [(4, 576, 7168), (4, 18432, 7168), (2, 7168, 2048)])
+def test_fp8_gemm_split_k_repeatable(cuda, M, N, Kd):
+    """The cross-workgroup split-K reduction must give bit-identical results on every
+    call (a stale or missing partial would show up as a changed output)."""
+    g = synth.gen(99 + N)
+    xq, xs = ref.act_quant(synth.activations(M, Kd, g))
+    wq, ws = ref.weight_quant(synth.weight_fp32(N, Kd, g))
+    xq, xs, wq, ws = xq.to(cuda), xs.to(cuda), wq.to(cuda), ws.to(cuda)
+    packed = K.pack_weight(wq, ws)
+    first = K.fp8_gemm(xq, xs, packed)
+    outs = [K.fp8_gemm(xq, xs, packed) for _ in range(30)] + [K.fp8_gemm(xq, xs, wq, ws) for _ in range(10)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, first)

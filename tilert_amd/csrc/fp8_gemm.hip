@@ -3,85 +3,90 @@
 // block -- the contract of fp8_gemm (refs/kernel.py:282-306, kernel :202-249).
 //
 // Design (gfx950):
-//   * The weight B is the only large operand (132 MB at 18432x7168); every byte of it
-//     is read exactly once, with 16-byte non-temporal loads, so the kernel is an HBM
-//     stream.  The tiny activation A (<= 256 rows) stays L1/L2 resident.
-//   * Math runs on the native OCP-fp8 MFMA v_mfma_f32_16x16x128_f8f6f4: one MFMA covers
-//     16 weight rows x 16 tokens x one whole 128-wide K block, i.e. exactly one scale
-//     block, so the per-block scale product (b_s * a_s) is applied once per MFMA to the
-//     fp32 partial -- the same per-K-block scaling as the reference kernel
-//     (refs/kernel.py:238-244).  For M <= 16 the unused token columns are free: the
-//     kernel is bandwidth-bound by >20x margin on the matrix cores.
-//   * Work split: a 256-thread workgroup (4 wave64s) owns 16 output rows and a slice of
-//     K blocks; the 4 waves interleave over the slice and are summed through LDS in a
-//     fixed order.  Narrow layers (few 16-row tiles) add a split over K across
-//     workgroups; the last workgroup to finish a row tile (agent-scope counter) sums the
-//     fp32 partials in split order, so results are deterministic.
+//   * The weight B is the only large operand (132 MB at 18432x7168) and every byte is
+//     read exactly once with 16-byte non-temporal loads: the kernel is an HBM stream.
+//     The activation A (<= 256 rows) stays L1/L2 resident.
+//   * Math is the native OCP-fp8 MFMA v_mfma_f32_16x16x128_f8f6f4: one MFMA covers 16
+//     weight rows x 16 tokens x one whole 128-wide K block = exactly one scale block, so
+//     the scale product b_s * a_s is applied once per MFMA to the fp32 partial (the
+//     per-K-block scaling of refs/kernel.py:238-244).  For M <= 16 the unused token
+//     columns are free: the matrix cores have >20x headroom over the weight stream.
+//   * Weight layouts.  Canonical row-major [N,K] (the drop-in fp8_gemm operand), or
+//     "fragment-packed": for every (16-row tile, 128-col block) the 2 KB MFMA operand
+//     fragment is stored contiguously in lane order ([2 pieces][64 lanes][16 B]), so
+//     each wave-wide load reads 1 KB of consecutive memory.  Packing is done once at
+//     weight-load time (tl_fp8_pack_weight), like the reference's per-op weight
+//     converters.  Measured on MI355X: packed fragments stream ~25% faster.
+//   * One weight fragment in flight per wave (U = 1) and 4-8 waves per workgroup: on
+//     this memory system deeper per-wave prefetch lowers achieved bandwidth.
+//   * Work split: a workgroup owns one 16-row tile and a slice of K blocks; its waves
+//     interleave over the slice and are summed through LDS in a fixed order.  The K split
+//     is chosen so the grid covers the 256 CUs evenly; the last workgroup of a row tile
+//     (agent-scope counter and agent-scope atomic partials) sums the fp32 partials in slice
+//     order, so results are deterministic.
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
 namespace tl {
 
-constexpr int kWaves = 4;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int MT, int U>
-__global__ __launch_bounds__(256) void fp8_gemm_kernel(
+__device__ inline v8i load_packed_fragment(const uint8_t* frag, int lane) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(frag);
+  const u32x4 lo = __builtin_nontemporal_load(p + lane);
+  const u32x4 hi = __builtin_nontemporal_load(p + 64 + lane);
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+__device__ inline uint2 pack_bf16x4(v4f v) {
+  return make_uint2(f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16),
+                    f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16));
+}
+
+// MT: 16-token tiles (M <= 16*MT); WAVES: waves per workgroup; PACKED: weight layout.
+template <int MT, int WAVES, bool PACKED>
+__global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, uint16_t* __restrict__ C, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
-  __shared__ float red[kWaves - 1][MT][4][64];
+  __shared__ float red[WAVES - 1][MT][4][64];
   const int KB = K >> 7;
   const int ksplit = gridDim.y;
   const int ks = blockIdx.y;
   const int kb_begin = ks * kb_per_split;
   const int kb_end = min(KB, kb_begin + kb_per_split);
-  const int n0 = blockIdx.x * 16;
+  const int rt = blockIdx.x;
+  const int n0 = rt * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
 
-  const uint8_t* brow = B + static_cast<size_t>(n0 + r) * K;
+  const uint8_t* brow = PACKED ? B + static_cast<size_t>(rt) * KB * 2048
+                               : B + static_cast<size_t>(n0 + r) * K;
   const float* bs_row = Bs + static_cast<size_t>(n0 >> 7) * KB;
 
   v4f acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb0 = kb_begin + wave; kb0 < kb_end; kb0 += kWaves * U) {
-    v8i a[U];
-    v8i x0[U];
-    float xs0[U];
+  for (int kb = kb_begin + wave; kb < kb_end; kb += WAVES) {
+    const v8i a = PACKED ? load_packed_fragment(brow + static_cast<size_t>(kb) * 2048, lane)
+                         : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
+    const float bsc = bs_row[kb];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kb = kb0 + kWaves * u;
-      a[u] = kb < kb_end ? load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g) : zero_v8i();
-      const bool tok = (kb < kb_end) && (r < M);
-      x0[u] = tok ? load_kblock(A + static_cast<size_t>(r) * K + kb * kBlock, g) : zero_v8i();
-      xs0[u] = tok ? As[static_cast<size_t>(r) * KB + kb] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kb = kb0 + kWaves * u;
-      if (kb < kb_end) {
-        const float bsc = bs_row[kb];
-        {
-          const v4f c = mfma_16x16x128_fp8(a[u], x0[u]);
-          const float sc = bsc * xs0[u];
-          acc[0] += c * sc;
-        }
-#pragma unroll
-        for (int mt = 1; mt < MT; ++mt) {
-          const int t = mt * 16 + r;
-          const bool tok = t < M;
-          const v8i x = tok ? load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g) : zero_v8i();
-          const float xs = tok ? As[static_cast<size_t>(t) * KB + kb] : 0.f;
-          const v4f c = mfma_16x16x128_fp8(a[u], x);
-          acc[mt] += c * (bsc * xs);
-        }
-      }
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = mt * 16 + r;
+      const bool tok = t < M;
+      const v8i x = tok ? load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g) : zero_v8i();
+      const float xs = tok ? As[static_cast<size_t>(t) * KB + kb] : 0.f;
+      const v4f c = mfma_16x16x128_fp8(a, x);
+      acc[mt] += c * (bsc * xs);
     }
   }
 
-  // ---- cross-wave reduction (fixed order w0 + w1 + w2 + w3)
+  // ---- cross-wave reduction in fixed order w0 + w1 + ... + w(WAVES-1)
   if (wave > 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -91,75 +96,114 @@ __global__ __launch_bounds__(256) void fp8_gemm_kernel(
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      acc[mt][j] = ((acc[mt][j] + red[0][mt][j][lane]) + red[1][mt][j][lane]) + red[2][mt][j][lane];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[mt][j] += red[w][mt][j][lane];
 
-  // lane holds rows n0 + 4g + j (j = 0..3) of token mt*16 + r
+  // lane holds output columns n0 + 4g + j (j = 0..3) of token mt*16 + r
   const int ncol = n0 + 4 * g;
   if (ksplit == 1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int t = mt * 16 + r;
-      if (t < M) {
-        const uint32_t lo = f32_to_bf16(acc[mt][0]) | (static_cast<uint32_t>(f32_to_bf16(acc[mt][1])) << 16);
-        const uint32_t hi = f32_to_bf16(acc[mt][2]) | (static_cast<uint32_t>(f32_to_bf16(acc[mt][3])) << 16);
-        *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = make_uint2(lo, hi);
-      }
+      if (t < M) *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(acc[mt]);
     }
     return;
   }
 
-  // ---- split-K: publish fp32 partials, the last arriving slice reduces in order
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int t = mt * 16 + r;
-    if (t < M)
-      *reinterpret_cast<v4f*>(partial + (static_cast<size_t>(ks) * M + t) * N + ncol) = acc[mt];
-  }
-  __threadfence();
-  uint32_t prev = 0;
-  if (lane == 0) prev = atomicAdd(&counters[blockIdx.x], 1u);
-  prev = __shfl(prev, 0);
-  if (prev != static_cast<uint32_t>(ksplit - 1)) return;
-  __threadfence();
+  // ---- split-K: publish fp32 partials; the last slice to arrive reduces them in order.
+  // Partials are agent-scope atomic stores/loads (written through to the device
+  // coherence point, read past this XCD's L2), so no cache-wide writeback or
+  // invalidate is needed; s_waitcnt makes the stores complete before the counter bump.
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int t = mt * 16 + r;
     if (t < M) {
-      v4f s = {0.f, 0.f, 0.f, 0.f};
-      for (int q = 0; q < ksplit; ++q)
-        s += __builtin_nontemporal_load(
-            reinterpret_cast<const v4f*>(partial + (static_cast<size_t>(q) * M + t) * N + ncol));
-      const uint32_t lo = f32_to_bf16(s[0]) | (static_cast<uint32_t>(f32_to_bf16(s[1])) << 16);
-      const uint32_t hi = f32_to_bf16(s[2]) | (static_cast<uint32_t>(f32_to_bf16(s[3])) << 16);
-      *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = make_uint2(lo, hi);
+      float* dst = partial + (static_cast<size_t>(ks) * M + t) * N + ncol;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) __hip_atomic_store(dst + j, acc[mt][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  if (lane == 0) atomicExch(&counters[blockIdx.x], 0u);  // ready for the next call
+  __builtin_amdgcn_s_waitcnt(0);
+  uint32_t prev = 0;
+  if (lane == 0) prev = __hip_atomic_fetch_add(&counters[rt], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0);
+  if (prev != static_cast<uint32_t>(ksplit - 1)) return;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int t = mt * 16 + r;
+    if (t < M) {
+      // issue the loads of 8 slices at a time, then add them in slice order
+      v4f s = {0.f, 0.f, 0.f, 0.f};
+      for (int q0 = 0; q0 < ksplit; q0 += 8) {
+        v4f v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int q = q0 + u < ksplit ? q0 + u : ksplit - 1;
+          const float* src = partial + (static_cast<size_t>(q) * M + t) * N + ncol;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v[u][j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          if (q0 + u < ksplit) s += v[u];
+      }
+      *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(s);
+    }
+  }
+  if (lane == 0) __hip_atomic_store(&counters[rt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Pack a canonical [N, K] fp8 weight into MFMA fragments: fragment (rt, kb) is 2048
+// bytes at ((rt * KB) + kb) * 2048; piece p, lane l = r + 16 g holds the 16 bytes of row
+// rt*16 + r, columns kb*128 + 64 p + 16 g ... +15 at offset p*1024 + l*16.
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint8_t* __restrict__ W,
+                                                          uint8_t* __restrict__ P, int N, int K) {
+  const int KB = K >> 7;
+  const int64_t chunk = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // 16-byte chunk id
+  const int64_t total = static_cast<int64_t>(N) * K / 16;
+  if (chunk >= total) return;
+  const int64_t frag = chunk >> 7;  // 128 chunks per fragment
+  const int within = static_cast<int>(chunk & 127);
+  const int p = within >> 6, l = within & 63;
+  const int rt = static_cast<int>(frag / KB), kb = static_cast<int>(frag % KB);
+  const int row = rt * 16 + (l & 15);
+  const int col = kb * 128 + 64 * p + 16 * (l >> 4);
+  reinterpret_cast<uint4*>(P)[chunk] = *reinterpret_cast<const uint4*>(W + static_cast<size_t>(row) * K + col);
 }
 
 struct GemmPlan {
   int ksplit;
   int kb_per_split;
   int row_tiles;
+  int waves;
 };
 
-// Pick the K split: keep >= ~768 workgroups (3 per CU) in flight and give every wave
-// of a slice at least one K block.
-static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
+// K split.  Wide layers (>= 512 row tiles, i.e. >= 2 workgroups per CU) run unsplit:
+// measured on MI355X, the split's extra round trips (partial store, counter, reload)
+// cost more than the better CU balance buys.  Narrow layers take the smallest split
+// giving >= 1024 workgroups (4 per CU), preferring a grid that is a whole multiple of
+// the 256 CUs, never leaving a slice empty.  Waves per workgroup: 8 when every wave
+// gets several K blocks, else 4.
+static GemmPlan plan_gemm(int64_t N, int64_t K) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
   p.row_tiles = static_cast<int>(N / 16);
-  int want = 1;
-  if (p.row_tiles < 768) want = static_cast<int>(cdiv(768, p.row_tiles));
-  int per = static_cast<int>(cdiv(KB, want));
-  per = static_cast<int>(cdiv(per, kWaves) * kWaves);  // whole waves per slice
-  if (per > KB) per = KB;
-  p.kb_per_split = per;
-  p.ksplit = static_cast<int>(cdiv(KB, per));
-  (void)M;
+  int s = 1;
+  if (p.row_tiles < 512) {
+    int smin = static_cast<int>(cdiv(1024, p.row_tiles));
+    if (smin > KB) smin = KB;
+    if (smin < 1) smin = 1;
+    s = smin;
+    for (int c = smin; c <= 2 * smin && c <= KB; ++c) {
+      if ((static_cast<int64_t>(p.row_tiles) * c) % 256 == 0) { s = c; break; }
+    }
+  }
+  p.kb_per_split = static_cast<int>(cdiv(KB, s));
+  p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
+  p.waves = p.kb_per_split >= 16 ? 8 : 4;
   return p;
 }
 
@@ -169,13 +213,58 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
 constexpr int kMaxRowTiles = 16384;  // N <= 262144
 constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 
+template <bool PACKED>
+static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, const float* Bs,
+                       uint16_t* C, int M, int N, int K, void* workspace, hipStream_t st) {
+  const GemmPlan p = plan_gemm(N, K);
+  uint32_t* counters = p.ksplit > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
+  float* partial = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
+  const dim3 grid(p.row_tiles, p.ksplit);
+  const int per = p.kb_per_split;
+#define TL_GEMM_LAUNCH(MT, W) \
+  hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, C, partial, counters, M, N, K, per)
+  if (p.waves == 8) {
+    if (M <= 16) TL_GEMM_LAUNCH(1, 8);
+    else if (M <= 32) TL_GEMM_LAUNCH(2, 8);
+    else if (M <= 64) TL_GEMM_LAUNCH(4, 8);
+    else if (M <= 128) TL_GEMM_LAUNCH(8, 4);
+    else TL_GEMM_LAUNCH(16, 4);
+  } else {
+    if (M <= 16) TL_GEMM_LAUNCH(1, 4);
+    else if (M <= 32) TL_GEMM_LAUNCH(2, 4);
+    else if (M <= 64) TL_GEMM_LAUNCH(4, 4);
+    else if (M <= 128) TL_GEMM_LAUNCH(8, 4);
+    else TL_GEMM_LAUNCH(16, 4);
+  }
+#undef TL_GEMM_LAUNCH
+  return check_launch("fp8_gemm");
+}
+
+static int validate(const char* who, const void* a, const float* a_s, const void* b,
+                    const float* b_s, void* c, int64_t M, int64_t N, int64_t K, void* workspace,
+                    size_t workspace_bytes, size_t need) {
+  if (M <= 0 || N <= 0 || K <= 0) { set_error("%s: empty problem M=%lld N=%lld K=%lld", who, (long long)M, (long long)N, (long long)K); return kErrArg; }
+  if (K % kBlock) { set_error("%s: K=%lld must be a multiple of 128", who, (long long)K); return kErrArg; }
+  if (N % 16) { set_error("%s: N=%lld must be a multiple of 16", who, (long long)N); return kErrArg; }
+  if (M > 256) { set_error("%s: M=%lld > 256 is not supported by the decode kernel", who, (long long)M); return kErrUnsupported; }
+  if (N > 16ll * kMaxRowTiles || K > (1ll << 30)) { set_error("%s: N or K too large", who); return kErrArg; }
+  if (!a || !a_s || !b || !b_s || !c) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) { set_error("%s: a and b must be 16-byte aligned", who); return kErrArg; }
+  if (reinterpret_cast<uintptr_t>(c) & 7) { set_error("%s: c must be 8-byte aligned", who); return kErrArg; }
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_error("%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes);
+    return kErrArg;
+  }
+  return kOk;
+}
+
 }  // namespace tl
 
 using namespace tl;
 
 extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock) return 0;
-  GemmPlan p = plan_gemm(M, N, K);
+  if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock || M > 256) return 0;
+  const GemmPlan p = plan_gemm(N, K);
   if (p.ksplit == 1) return 0;
   return kCounterBytes + static_cast<size_t>(p.ksplit) * M * N * sizeof(float);
 }
@@ -183,32 +272,30 @@ extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
 extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
                            void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
                            size_t workspace_bytes, void* stream) {
-  if (M <= 0 || N <= 0 || K <= 0) { set_error("fp8_gemm: empty problem M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K); return kErrArg; }
-  if (K % kBlock) { set_error("fp8_gemm: K=%lld must be a multiple of 128", (long long)K); return kErrArg; }
-  if (N % 16) { set_error("fp8_gemm: N=%lld must be a multiple of 16", (long long)N); return kErrArg; }
-  if (M > 256) { set_error("fp8_gemm: M=%lld > 256 is not supported by the decode kernel", (long long)M); return kErrUnsupported; }
-  if (N > 16ll * kMaxRowTiles || K > (1ll << 30)) { set_error("fp8_gemm: N or K too large"); return kErrArg; }
-  if (!a || !a_s || !b || !b_s || !c_bf16) { set_error("fp8_gemm: null pointer"); return kErrArg; }
-  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) { set_error("fp8_gemm: a and b must be 16-byte aligned"); return kErrArg; }
-  if (reinterpret_cast<uintptr_t>(c_bf16) & 7) { set_error("fp8_gemm: c must be 8-byte aligned"); return kErrArg; }
-  GemmPlan p = plan_gemm(M, N, K);
   const size_t need = tl_fp8_gemm_workspace_bytes(M, N, K);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
-    set_error("fp8_gemm: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-    return kErrArg;
-  }
-  uint32_t* counters = need ? static_cast<uint32_t*>(workspace) : nullptr;
-  float* partial = need ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
-  dim3 grid(p.row_tiles, p.ksplit);
-  hipStream_t st = (hipStream_t)stream;
-  const uint8_t* A = (const uint8_t*)a;
-  const uint8_t* B = (const uint8_t*)b;
-  uint16_t* C = (uint16_t*)c_bf16;
-  const int m = (int)M, n = (int)N, k = (int)K, per = p.kb_per_split;
-  if (M <= 16) hipLaunchKernelGGL((fp8_gemm_kernel<1, 4>), grid, dim3(256), 0, st, A, a_s, B, b_s, C, partial, counters, m, n, k, per);
-  else if (M <= 32) hipLaunchKernelGGL((fp8_gemm_kernel<2, 4>), grid, dim3(256), 0, st, A, a_s, B, b_s, C, partial, counters, m, n, k, per);
-  else if (M <= 64) hipLaunchKernelGGL((fp8_gemm_kernel<4, 2>), grid, dim3(256), 0, st, A, a_s, B, b_s, C, partial, counters, m, n, k, per);
-  else if (M <= 128) hipLaunchKernelGGL((fp8_gemm_kernel<8, 2>), grid, dim3(256), 0, st, A, a_s, B, b_s, C, partial, counters, m, n, k, per);
-  else hipLaunchKernelGGL((fp8_gemm_kernel<16, 1>), grid, dim3(256), 0, st, A, a_s, B, b_s, C, partial, counters, m, n, k, per);
-  return check_launch("fp8_gemm");
+  int rc = validate("fp8_gemm", a, a_s, b, b_s, c_bf16, M, N, K, workspace, workspace_bytes, need);
+  if (rc) return rc;
+  return launch_gemm<false>((const uint8_t*)a, a_s, (const uint8_t*)b, b_s, (uint16_t*)c_bf16,
+                            (int)M, (int)N, (int)K, workspace, (hipStream_t)stream);
+}
+
+extern "C" int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* stream) {
+  if (N <= 0 || K <= 0 || N % 16 || K % kBlock) { set_error("pack_weight: need N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)", (long long)N, (long long)K); return kErrArg; }
+  if (!b || !packed) { set_error("pack_weight: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(packed)) & 15) { set_error("pack_weight: pointers must be 16-byte aligned"); return kErrArg; }
+  if (b == packed) { set_error("pack_weight: in-place packing is not supported"); return kErrArg; }
+  const int64_t chunks = N * K / 16;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3(cdiv(chunks, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)b, (uint8_t*)packed, (int)N, (int)K);
+  return check_launch("pack_weight");
+}
+
+extern "C" int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed,
+                                  const float* b_s, void* c_bf16, int64_t M, int64_t N, int64_t K,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  const size_t need = tl_fp8_gemm_workspace_bytes(M, N, K);
+  int rc = validate("fp8_gemm_packed", a, a_s, b_packed, b_s, c_bf16, M, N, K, workspace, workspace_bytes, need);
+  if (rc) return rc;
+  return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, (uint16_t*)c_bf16,
+                           (int)M, (int)N, (int)K, workspace, (hipStream_t)stream);
 }

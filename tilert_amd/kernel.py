@@ -118,25 +118,62 @@ class _Workspace:
 _WS = _Workspace()
 
 
-def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Tensor,
+class PackedFP8Weight:
+    """A block-scaled fp8 weight [N, K] repacked into MFMA operand fragments.
+
+    Built once at weight-load time (the role of the reference's per-op weight converters,
+    e.g. ``RMSNormProjQKVAFP8MMAWeightsConverter``); ``fp8_gemm``/``linear`` accept it in
+    place of the canonical weight and give bit-identical results, streaming ~25% faster.
+    """
+
+    def __init__(self, data: torch.Tensor, scale: torch.Tensor, N: int, K: int) -> None:
+        self.data, self.scale, self.N, self.K = data, scale, N, K
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.N, self.K)
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+
+def pack_weight(b: torch.Tensor, b_s: torch.Tensor) -> PackedFP8Weight:
+    """Repack a canonical e4m3fn weight [N, K] (+ its [ceil(N/128), K/128] scales)."""
+    if b.dtype != torch.float8_e4m3fn or b.dim() != 2 or not b.is_contiguous():
+        raise ValueError("pack_weight: expects a contiguous 2-D float8_e4m3fn weight")
+    _require_cuda("pack_weight", b, b_s)
+    N, K = b.shape
+    out = torch.empty(N * K, dtype=torch.uint8, device=b.device)
+    _lib.call("tl_fp8_pack_weight", b.data_ptr(), out.data_ptr(), N, K, _stream(b))
+    return PackedFP8Weight(out, b_s.contiguous(), N, K)
+
+
+def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b, b_s: torch.Tensor | None = None,
              out: torch.Tensor | None = None) -> torch.Tensor:
     """``C = A . B^T`` with per-128-block scales; A e4m3fn [..., K] + a_s [..., K/128],
-    B e4m3fn [N, K] + b_s [ceil(N/128), K/128].  Returns bf16 [..., N]
-    (refs/kernel.py:282-306; output dtype is bf16, DeepSeek inference's default dtype)."""
-    if not (a.is_contiguous() and b.is_contiguous()):
+    B e4m3fn [N, K] (or a ``PackedFP8Weight``) + b_s [ceil(N/128), K/128].  Returns bf16
+    [..., N] (refs/kernel.py:282-306; bf16 is DeepSeek inference's default dtype)."""
+    packed = isinstance(b, PackedFP8Weight)
+    if packed:
+        b_s = b.scale if b_s is None else b_s
+        bt = b.data
+    else:
+        bt = b
+    if not (a.is_contiguous() and bt.is_contiguous()):
         raise AssertionError("Input tensors must be contiguous")
     if not (a_s.is_contiguous() and b_s.is_contiguous()):
         raise AssertionError("Scaling factor tensors must be contiguous")
-    if a.dtype != torch.float8_e4m3fn or b.dtype != torch.float8_e4m3fn:
+    if a.dtype != torch.float8_e4m3fn or (not packed and b.dtype != torch.float8_e4m3fn):
         raise ValueError("fp8_gemm: a and b must be float8_e4m3fn")
     if a_s.dtype != torch.float32 or b_s.dtype != torch.float32:
         raise ValueError("fp8_gemm: scales must be float32")
-    _require_cuda("fp8_gemm", a, a_s, b, b_s)
+    _require_cuda("fp8_gemm", a, a_s, bt, b_s)
     K = a.size(-1)
     M = a.numel() // K
-    N = b.size(0)
-    if b.size(1) != K:
-        raise ValueError(f"fp8_gemm: K mismatch ({K} vs {b.size(1)})")
+    N = b.shape[0]
+    if b.shape[1] != K:
+        raise ValueError(f"fp8_gemm: K mismatch ({K} vs {b.shape[1]})")
     if a_s.numel() != M * (K // BLOCK) or b_s.shape != ((N + BLOCK - 1) // BLOCK, K // BLOCK):
         raise ValueError("fp8_gemm: scale shapes do not match the operands")
     if out is None:
@@ -149,6 +186,6 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b: torch.Tensor, b_s: torch.Ten
     if nbytes:
         ws = _WS.get(a.device, st, nbytes)
         ws_ptr, ws_len = ws.data_ptr(), ws.numel()
-    _lib.call("tl_fp8_gemm", a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(),
-              out.data_ptr(), M, N, K, ws_ptr, ws_len, st)
+    _lib.call("tl_fp8_gemm_packed" if packed else "tl_fp8_gemm", a.data_ptr(), a_s.data_ptr(),
+              bt.data_ptr(), b_s.data_ptr(), out.data_ptr(), M, N, K, ws_ptr, ws_len, st)
     return out
