@@ -19,6 +19,7 @@
  *   tl_fp8_gemm         fp8_gemm             .../refs/kernel.py:282-306; the FP8 GEMVs behind
  *                       projx_wqkva_op (.../ops/projx_wqkva.py:22-48), rmsnorm_proj_qb_op,
  *                       unproj_o_allreduce_op, rmsnorm_up_gate_silu_op, down_allreduce_op
+ *   tl_fp8_pack_weight  the per-op weight converters (load-time layout change)
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
  *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
@@ -89,33 +90,39 @@ int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, co
                        void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
                        size_t workspace_bytes, void* stream);
 
-/* MoE gate/up + SwiGLU at one expert-parallel shard.
- * x fp8 [M, D] + x_s fp32 [M, D/128] (act_quant of the hidden state); per local expert e
- * (0 <= e < n_local) gate G_e and up U_e: fp8 [I, D] at gate + e*I*D, scales
- * [I/128, D/128] at gate_s + e*(I/128)*(D/128) (same for up).  topk_idx int32 [M, topk]
- * holds global expert ids; the shard owns ids [expert_begin, expert_begin + n_local).
- * Every local expert hit by at least one token gets a slot (slots in ascending expert
- * order); h bf16 [n_local, M, I] receives, for slot s and EVERY token t,
- * h[s,t,:] = bf16(silu(x_t . G^T) * (x_t . U^T)) (rows of unrouted tokens are computed
- * but ignored by tl_moe_down_combine).  M <= 16, D and I multiples of 128.
+/* MoE gate/up + SwiGLU at one expert-parallel shard (bf16 activations x fp8 weights,
+ * the reference MoE's BF16MMA numerics).
+ * x bf16 [M, D]; w13_packed = tl_fp8_pack_weight of the stacked per-expert gate/up
+ * weights [n_local * 2I, D] (expert e: rows e*2I .. e*2I+I-1 gate, then I rows up);
+ * s13 fp32 [n_local, 2I/128, D/128].  topk_idx int32 [M, topk] holds global expert ids;
+ * the shard owns ids [expert_begin, expert_begin + n_local).  Every local expert hit by
+ * at least one token gets a slot (ascending expert order); h bf16 [n_local, M, I]
+ * receives, for slot s < n_hit and EVERY token t,
+ *   h[s,t,:] = bf16(silu(x_t . G^T) * (x_t . U^T))  (fp32 products and SwiGLU),
+ * where G, U are the block-dequantised weights; rows of unrouted tokens are computed but
+ * ignored by tl_moe_down_combine; slots >= n_hit are not written.
+ * 1 <= M <= 16, n_local <= 64, D and I multiples of 128.
  * Replaces the grouped GEMM of expert_select_up_gate_silu_op
- * (expert_sel_up_gate_silu.py:23-48, golden :670-692); routing itself is an input. */
-int tl_moe_gate_up_swiglu(const void* x_fp8, const float* x_s, const void* gate,
-                          const float* gate_s, const void* up, const float* up_s,
+ * (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:23-48, golden :670-692); routing is an
+ * input. */
+int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed, const float* s13,
                           const int32_t* topk_idx, int64_t M, int64_t topk, int64_t expert_begin,
                           int64_t n_local, int64_t D, int64_t I, void* h_bf16, void* stream);
 
-/* MoE down projection + routing-weighted combine.
- * h bf16 [n_local, M, I] from tl_moe_gate_up_swiglu (act-quantised per 1x128 inside,
- * scale_mode as tl_act_quant); per local expert down D_e fp8 [D, I] at down + e*D*I,
- * scales [D/128, I/128]; topk_w fp32 [M, topk].
- * y[t] = bf16( sum_e bf16(w[t,e] * (hq[t,e] . D_e^T)) ), experts summed in ascending
- * order, 0 for tokens with no local expert.  Replaces expert_down_allreduce_op
- * (expert_down_allreduce.py:23-63, golden :455-468) at one shard (no allreduce). */
-int tl_moe_down_combine(const void* h_bf16, const void* down, const float* down_s,
+/* MoE down projection + routing-weighted combine at one shard.
+ * h bf16 [n_local, M, I] from tl_moe_gate_up_swiglu (same topk_idx); w2_packed =
+ * tl_fp8_pack_weight of the stacked down weights [n_local * D, I]; s2 fp32
+ * [n_local, D/128, I/128]; topk_w fp32 [M, topk].
+ *   y[t] = bf16( sum over the token's local experts e, ascending, of
+ *                bf16(w[t,e] * (h[t,e] . D_e^T)) )   (fp32 sum)
+ * y bf16 [M, D]; 0 for tokens with no local expert (the shard's partial of the
+ * allreduce).  Replaces expert_down_allreduce_op
+ * (deepseek_v3_2/ops/expert_down_allreduce.py:23-63, golden :455-468) without the
+ * cross-GPU allreduce. */
+int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, const float* s2,
                         const int32_t* topk_idx, const float* topk_w, int64_t M, int64_t topk,
                         int64_t expert_begin, int64_t n_local, int64_t D, int64_t I,
-                        int scale_mode, void* y_bf16, void* stream);
+                        void* y_bf16, void* stream);
 
 /* DSA lightning-indexer scores over an fp8 key cache.
  * q fp8 [M, H, 128]; q_s fp32 per token [M] (q_s_per_head = 0) or per (token, head)

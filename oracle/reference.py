@@ -147,24 +147,24 @@ def hit_experts(topk_idx: torch.Tensor, expert_begin: int, n_local: int) -> list
 def moe_gate_up(
     x: torch.Tensor,
     gq: torch.Tensor, gs: torch.Tensor, uq: torch.Tensor, us: torch.Tensor,
-    topk_idx: torch.Tensor, expert_begin: int, scale_mode: int = 0,
+    topk_idx: torch.Tensor, expert_begin: int,
 ) -> tuple[torch.Tensor, list[int]]:
     """Grouped gate/up + SwiGLU for every hit local expert and every token.
 
-    Per (token, expert): ``h = bf16(silu(x.G^T) * (x.U^T))`` with fp32 products -- the
-    per-expert loop of ``ExpertSelectUpGateSiLU.golden_forward``
-    (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:670-692), at the W8A8 precision of
-    BASELINE config 2 (x act-quantised per 1x128, weights 128x128 block-scaled).
+    ``ExpertSelectUpGateSiLU.golden_forward`` (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:
+    670-692) with its reference weights (``init_reference_weights`` :545-552: each expert's
+    fp8 weight dequantised per 128x128 block, then rounded to bf16): per (token, expert)
+    ``h = bf16(silu(x.float() @ G.float().T) * (x.float() @ U.float().T))``.  x is bf16 and
+    NOT quantised (the reference MoE runs BF16MMA, deepseek_v3_2/modules/moe.py:32-45).
     Returns h [n_hit, M, I] bf16 (slot order = ascending local expert id) and the hit list.
     """
     E = gq.shape[0]
-    xq, xs = act_quant(x, BLOCK, scale_mode)
-    xd = act_dequant(xq, xs)
+    xf = x.float()
     hits = hit_experts(topk_idx, expert_begin, E)
     hs = []
     for e in hits:
-        g = xd @ weight_dequant(gq[e], gs[e]).T
-        u = xd @ weight_dequant(uq[e], us[e]).T
+        g = xf @ weight_dequant(gq[e], gs[e]).to(torch.bfloat16).float().T
+        u = xf @ weight_dequant(uq[e], us[e]).to(torch.bfloat16).float().T
         hs.append(swiglu(g, u).to(torch.bfloat16))
     I = gq.shape[1]
     h = torch.stack(hs) if hs else torch.zeros(0, x.shape[0], I, dtype=torch.bfloat16)
@@ -174,35 +174,35 @@ def moe_gate_up(
 def moe_down(
     h: torch.Tensor, hits: list[int],
     dq: torch.Tensor, ds: torch.Tensor,
-    topk_idx: torch.Tensor, topk_w: torch.Tensor, expert_begin: int, scale_mode: int = 0,
+    topk_idx: torch.Tensor, topk_w: torch.Tensor, expert_begin: int,
 ) -> torch.Tensor:
     """Down projection + routing-weighted sum over the local experts.
 
-    ``y[t] = bf16( sum_e bf16(w[t,e] * (h[t,e] . D_e^T)) )`` -- the order of
-    ``ExpertDownAllReduce.golden_forward`` (deepseek_v3_2/ops/expert_down_allreduce.py:455-468:
-    each weighted expert term cast to bf16, then summed), with h act-quantised per 1x128
-    for the FP8 down GEMM.  Terms are summed in fp32 in ascending expert order.
+    ``ExpertDownAllReduce.golden_forward`` (deepseek_v3_2/ops/expert_down_allreduce.py:
+    455-468, weights rounded to bf16 after dequantisation as in :389-393): each term
+    ``bf16(w[t,e] * (h[t,e].float() @ D_e.float().T))``, summed over the token's local
+    experts in fp32 (ascending expert order) and rounded once to bf16.  Tokens with no
+    local expert get 0 (the shard's share; the cross-shard sum is the allreduce).
     """
     M = topk_idx.shape[0]
     D = dq.shape[1]
     acc = torch.zeros(M, D, dtype=torch.float32)
     pairs = local_pairs(topk_idx, expert_begin, dq.shape[0])
     slot = {e: i for i, e in enumerate(hits)}
-    wd = {e: weight_dequant(dq[e], ds[e]) for e in hits}
     for e in hits:
+        wd = weight_dequant(dq[e], ds[e]).to(torch.bfloat16).float()
         for (t, j, ee) in pairs:
             if ee != e:
                 continue
-            hq, hsc = act_quant(h[slot[e], t][None], BLOCK, scale_mode)
-            term = act_dequant(hq, hsc)[0] @ wd[e].T
+            term = h[slot[e], t].float() @ wd.T
             acc[t] += (term * topk_w[t, j].float()).to(torch.bfloat16).float()
     return acc.to(torch.bfloat16)
 
 
-def moe_forward(x, gq, gs, uq, us, dq, ds, topk_idx, topk_w, expert_begin, scale_mode=0):
+def moe_forward(x, gq, gs, uq, us, dq, ds, topk_idx, topk_w, expert_begin):
     """Whole local-expert MoE layer (config 2): gate/up + SwiGLU, down, weighted sum."""
-    h, hits = moe_gate_up(x, gq, gs, uq, us, topk_idx, expert_begin, scale_mode)
-    return moe_down(h, hits, dq, ds, topk_idx, topk_w, expert_begin, scale_mode)
+    h, hits = moe_gate_up(x, gq, gs, uq, us, topk_idx, expert_begin)
+    return moe_down(h, hits, dq, ds, topk_idx, topk_w, expert_begin)
 
 
 def indexer_scores(

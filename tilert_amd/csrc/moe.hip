@@ -1,0 +1,271 @@
+// MoE expert layer at one expert-parallel shard: grouped gate/up GEMM with fused SwiGLU,
+// then the down GEMM with the routing-weighted combine.
+//
+// Numerics follow the reference MoE (BF16MMA: bf16 activations, fp8 weights dequantised
+// per 128x128 block; expert_sel_up_gate_silu.py:670-692, expert_down_allreduce.py:455-468).
+// Each fp8 weight is dequantised in registers exactly as the reference's golden weights
+// are built (init_reference_weights, expert_sel_up_gate_silu.py:545-552:
+// bf16(fp32(q) * block_scale), round-to-nearest-even) and multiplied on the bf16 MFMA
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation over the whole K -- so the products
+// are the reference's products and only the fp32 summation order differs.
+// (v_cvt_scalef32_pk_bf16_fp8 cannot do this: it applies only the scale's exponent.)
+//
+// Routing is an input (token -> 8 global expert ids).  Every kernel derives the shard's
+// hit-expert set on the device from topk_idx, so no host synchronisation is needed: a
+// local expert hit by any token gets a "slot" (ascending expert order); only hit experts'
+// weights are read.  With M <= 16 tokens the MFMA's 16 columns cover every token, so
+// each hit expert is evaluated for all tokens (unrouted rows are ignored by the combine).
+//
+// Weight layout: the fragment-packed layout of tl_fp8_pack_weight applied to the stacked
+// per-expert matrices: gate/up as w13 [E][2I rows (gate then up)][D], down as
+// w2 [E][D rows][I]; scales [E][2I/128][D/128] and [E][D/128][I/128].
+#include "common.h"
+#include "../../include/tilert_amd.h"
+
+namespace tl {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMoeWaves = 4;
+constexpr int kMaxLocalExperts = 64;
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ inline uint32_t bf16x2_bits(v2f f) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));  // v_cvt_pk_bf16_f32, RNE
+}
+
+// fp8 dwords d0, d1 (8 weights, k order = byte order) -> bf16(fp32(q) * s) MFMA operand.
+__device__ inline v8bf dequant8_bf16(uint32_t d0, uint32_t d1, float s) {
+  u32x4 r;
+  r.x = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, false) * s);
+  r.y = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, true) * s);
+  r.z = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, false) * s);
+  r.w = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, true) * s);
+  return __builtin_bit_cast(v8bf, r);
+}
+
+__device__ inline v8i load_fragment(const uint8_t* frag, int lane) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(frag);
+  const u32x4 lo = __builtin_nontemporal_load(p + lane);
+  const u32x4 hi = __builtin_nontemporal_load(p + 64 + lane);
+  v8i r;
+  r[0] = lo.x; r[1] = lo.y; r[2] = lo.z; r[3] = lo.w;
+  r[4] = hi.x; r[5] = hi.y; r[6] = hi.z; r[7] = hi.w;
+  return r;
+}
+
+// The bf16 activation operand matching a packed weight fragment: lane group g holds
+// K offsets {16g..16g+15} and {64+16g..64+16g+15} of the block, as 4 groups of 8.
+struct ActOperand {
+  v8bf v[4];
+};
+
+__device__ inline ActOperand load_act(const uint16_t* row_kblock, int g, bool live) {
+  ActOperand o;
+  const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u32x4 d = {0u, 0u, 0u, 0u};
+    if (live) d = *reinterpret_cast<const u32x4*>(row_kblock + off[j]);
+    o.v[j] = __builtin_bit_cast(v8bf, d);
+  }
+  return o;
+}
+
+// acc[16 rows x 16 tokens] += dequant(W block) . x over one 128-wide K block: 4 chained
+// bf16 MFMAs on the block's bf16-rounded dequantised weights.
+__device__ inline v4f mfma_block_bf16(const v8i& w, float scale, const ActOperand& x, v4f acc) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(w[2 * j], w[2 * j + 1], scale), x.v[j], acc, 0, 0, 0);
+  return acc;
+}
+
+// Hit-expert bitmask of this shard, computed by the whole workgroup.
+__device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, int pairs, int e0,
+                                        int n_local, uint32_t* s_words) {
+  if (threadIdx.x < 2) s_words[threadIdx.x] = 0u;
+  __syncthreads();
+  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+    const int e = topk_idx[i] - e0;
+    if (e >= 0 && e < n_local) atomicOr(&s_words[e >> 5], 1u << (e & 31));
+  }
+  __syncthreads();
+  const uint64_t m = static_cast<uint64_t>(s_words[0]) | (static_cast<uint64_t>(s_words[1]) << 32);
+  __syncthreads();
+  return m;
+}
+
+__device__ inline int nth_set_bit(uint64_t m, int n) {
+  for (int i = 0; i < n; ++i) m &= m - 1;
+  return __builtin_ctzll(m);
+}
+
+__device__ inline float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// ---------------------------------------------------------------------- gate/up
+// Work item = (slot, 16-channel tile); a persistent grid strides over n_hit * I/16 items.
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13, const float* __restrict__ s13,
+    const int32_t* __restrict__ topk_idx, int M, int topk, int e0, int n_local, int D, int I,
+    uint16_t* __restrict__ h) {
+  __shared__ uint32_t s_words[2];
+  __shared__ float red[kMoeWaves - 1][2][4][64];
+  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local, s_words);
+  const int n_hit = __builtin_popcountll(mask);
+  const int KB = D >> 7;
+  const int tiles = I >> 4;
+  const int rows_e = 2 * I;  // gate rows then up rows
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const bool tok = r < M;
+  const uint16_t* xrow = x + static_cast<size_t>(tok ? r : 0) * D;
+
+  for (int item = blockIdx.x; item < n_hit * tiles; item += gridDim.x) {
+    const int slot = item / tiles, rt = item - slot * tiles;
+    const int e = nth_set_bit(mask, slot);
+    const uint8_t* gate = w13 + (static_cast<size_t>(e) * (rows_e >> 4) + rt) * KB * 2048;
+    const uint8_t* up = gate + static_cast<size_t>(tiles) * KB * 2048;
+    const float* gs = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((rt * 16) >> 7)) * KB;
+    const float* us = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((I + rt * 16) >> 7)) * KB;
+    v4f ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = wave; kb < KB; kb += kMoeWaves) {
+      const v8i wg = load_fragment(gate + static_cast<size_t>(kb) * 2048, lane);
+      const v8i wu = load_fragment(up + static_cast<size_t>(kb) * 2048, lane);
+      const ActOperand xa = load_act(xrow + kb * kBlock, g, tok);
+      ag = mfma_block_bf16(wg, gs[kb], xa, ag);
+      au = mfma_block_bf16(wu, us[kb], xa, au);
+    }
+    if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[wave - 1][0][j][lane] = ag[j];
+        red[wave - 1][1][j][lane] = au[j];
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < kMoeWaves - 1; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ag[j] += red[w][0][j][lane];
+          au[j] += red[w][1][j][lane];
+        }
+      if (tok) {
+        uint16_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16(silu(ag[j]) * au[j]);
+        uint16_t* dst = h + (static_cast<size_t>(slot) * M + r) * I + rt * 16 + 4 * g;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                    o[2] | (static_cast<uint32_t>(o[3]) << 16));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------- down + combine
+// One workgroup per 16-row output tile; slots are visited in ascending order and each
+// expert's term is reduced across waves, weighted, rounded to bf16 and accumulated in
+// fp32 -- a fixed order, so the result is deterministic.
+__global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(
+    const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int M, int topk, int e0,
+    int n_local, int D, int I, uint16_t* __restrict__ y) {
+  __shared__ uint32_t s_words[2];
+  __shared__ float red[kMoeWaves - 1][4][64];
+  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local, s_words);
+  const int n_hit = __builtin_popcountll(mask);
+  const int KB = I >> 7;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const bool tok = r < M;
+  const int rt = blockIdx.x;
+  v4f yacc = {0.f, 0.f, 0.f, 0.f};
+
+  for (int slot = 0; slot < n_hit; ++slot) {
+    const int e = nth_set_bit(mask, slot);
+    const uint8_t* wt = w2 + (static_cast<size_t>(e) * (D >> 4) + rt) * KB * 2048;
+    const float* sc = s2 + (static_cast<size_t>(e) * (D >> 7) + ((rt * 16) >> 7)) * KB;
+    const uint16_t* hrow = h + (static_cast<size_t>(slot) * M + (tok ? r : 0)) * I;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb = wave; kb < KB; kb += kMoeWaves) {
+      const v8i w = load_fragment(wt + static_cast<size_t>(kb) * 2048, lane);
+      const ActOperand xa = load_act(hrow + kb * kBlock, g, tok);
+      acc = mfma_block_bf16(w, sc[kb], xa, acc);
+    }
+    if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[wave - 1][j][lane] = acc[j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < kMoeWaves - 1; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] += red[w][j][lane];
+      // routing weight of (token r, expert e); 0 when the token does not use it
+      float wr = 0.f;
+      if (tok)
+        for (int k = 0; k < topk; ++k)
+          if (topk_idx[r * topk + k] == e + e0) wr = topk_w[r * topk + k];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) yacc[j] += bf16_to_f32(f32_to_bf16(acc[j] * wr));
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && tok) {
+    uint16_t* dst = y + static_cast<size_t>(r) * D + rt * 16 + 4 * g;
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(f32_to_bf16(yacc[0]) | (static_cast<uint32_t>(f32_to_bf16(yacc[1])) << 16),
+                   f32_to_bf16(yacc[2]) | (static_cast<uint32_t>(f32_to_bf16(yacc[3])) << 16));
+  }
+}
+
+static int check_moe(const char* who, int64_t M, int64_t topk, int64_t n_local, int64_t D, int64_t I) {
+  if (M < 1 || M > 16) { set_error("%s: M=%lld must be in [1, 16]", who, (long long)M); return kErrUnsupported; }
+  if (topk < 1 || topk > 64) { set_error("%s: topk=%lld must be in [1, 64]", who, (long long)topk); return kErrArg; }
+  if (n_local < 1 || n_local > kMaxLocalExperts) { set_error("%s: n_local=%lld must be in [1, %d]", who, (long long)n_local, kMaxLocalExperts); return kErrUnsupported; }
+  if (D <= 0 || I <= 0 || D % kBlock || I % kBlock) { set_error("%s: D=%lld and I=%lld must be positive multiples of 128", who, (long long)D, (long long)I); return kErrArg; }
+  if (D > (1 << 20) || I > (1 << 20)) { set_error("%s: D or I too large", who); return kErrArg; }
+  return kOk;
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+extern "C" int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed, const float* s13,
+                                     const int32_t* topk_idx, int64_t M, int64_t topk,
+                                     int64_t expert_begin, int64_t n_local, int64_t D, int64_t I,
+                                     void* h_bf16, void* stream) {
+  int rc = check_moe("moe_gate_up_swiglu", M, topk, n_local, D, I);
+  if (rc) return rc;
+  if (!x_bf16 || !w13_packed || !s13 || !topk_idx || !h_bf16) { set_error("moe_gate_up_swiglu: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed)) & 15) { set_error("moe_gate_up_swiglu: x and weights must be 16-byte aligned"); return kErrArg; }
+  // enough workgroups for the largest possible hit set, capped at 4 per CU
+  const int64_t max_items = n_local * (I / 16);
+  const int grid = static_cast<int>(max_items < 1024 ? max_items : 1024);
+  hipLaunchKernelGGL(moe_gate_up_kernel, dim3(grid), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx, (int)M, (int)topk,
+                     (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
+  return check_launch("moe_gate_up_swiglu");
+}
+
+extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, const float* s2,
+                                   const int32_t* topk_idx, const float* topk_w, int64_t M,
+                                   int64_t topk, int64_t expert_begin, int64_t n_local, int64_t D,
+                                   int64_t I, void* y_bf16, void* stream) {
+  int rc = check_moe("moe_down_combine", M, topk, n_local, D, I);
+  if (rc) return rc;
+  if (!h_bf16 || !w2_packed || !s2 || !topk_idx || !topk_w || !y_bf16) { set_error("moe_down_combine: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15) { set_error("moe_down_combine: h and weights must be 16-byte aligned"); return kErrArg; }
+  hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
+                     (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
+                     (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)y_bf16);
+  return check_launch("moe_down_combine");
+}

@@ -142,7 +142,7 @@ def pack_weight(b: torch.Tensor, b_s: torch.Tensor) -> PackedFP8Weight:
     """Repack a canonical e4m3fn weight [N, K] (+ its [ceil(N/128), K/128] scales)."""
     if b.dtype != torch.float8_e4m3fn or b.dim() != 2 or not b.is_contiguous():
         raise ValueError("pack_weight: expects a contiguous 2-D float8_e4m3fn weight")
-    _require_cuda("pack_weight", b, b_s)
+    _require_cuda("pack_weight", b)
     N, K = b.shape
     out = torch.empty(N * K, dtype=torch.uint8, device=b.device)
     _lib.call("tl_fp8_pack_weight", b.data_ptr(), out.data_ptr(), N, K, _stream(b))
