@@ -136,11 +136,15 @@ int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
                           int64_t cur_pos, void* stream);
 
 /* Exact per-row top-k.  logits fp32 [rows, ld]; row i considers columns
- * [0, valid_base + 1 + i) (capped at ld) -- topk_accurate's convention with
- * valid_base = seq_len - num_samples (ops/topk.py:77-80,101).  out int32 [rows, k]:
- * indices in descending score order (ties: ascending index), -1 past the valid length.
- * workspace of tl_topk_workspace_bytes(rows, ld, k) bytes (no initialisation needed).
- * Replaces topk_accurate_op (ops/topk.py:62-109). */
+ * [0, valid_base + 1 + i) (clamped to [0, ld]) -- topk_accurate's convention with
+ * valid_base = seq_len - num_samples (ops/topk.py:77-80,101).  out int32 [rows, k]
+ * receives the k selected column indices in ASCENDING INDEX order: every column whose
+ * score is above the k-th largest, plus the lowest-index columns equal to it; when a
+ * row has fewer than k valid columns, all of them, then -1.  The selected set is exactly
+ * torch.topk's (ops/topk.py:128-143) up to the choice among exact ties, which is
+ * lowest-index-first here.  1 <= k <= 8192.  workspace: tl_topk_workspace_bytes(rows,
+ * ld, k) bytes, ZERO-FILLED before first use and left zeroed by every call; calls sharing
+ * it must be ordered.  Replaces topk_accurate_op (ops/topk.py:62-109). */
 size_t tl_topk_workspace_bytes(int64_t rows, int64_t ld, int64_t k);
 int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64_t valid_base, int64_t k,
                  int32_t* out, void* workspace, size_t workspace_bytes, void* stream);

@@ -1,0 +1,90 @@
+"""DSA lightning indexer over an fp8 key cache, with the reference's operator shapes
+(ops/sparse_index.py:11-128): ``sparse_index`` fills the logits, ``sparse_index_topk``
+also selects the top-k key positions per token.
+
+The reference's native op takes a bf16 cache and bf16 q (ops/sparse_index.py:40-47);
+this is its fp8 variant: q e4m3fn with a per-token (or per-(token, head)) fp32 scale,
+keys e4m3fn [L, 128] with a per-key fp32 scale (the fp8 KI cache of
+pd_vllm/profiles/mla_nsa.py:17-41,211-228, flattened).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .kernel import _require_cuda, _stream
+from .topk import topk_rows
+
+
+def _check(q, q_scale, kv, k_scale, weights, logits, heads=(32, 64)):
+    if q.dtype != torch.float8_e4m3fn:
+        raise ValueError("q must be a float8_e4m3fn tensor.")
+    if kv.dtype != torch.float8_e4m3fn:
+        raise ValueError("kv must be a float8_e4m3fn tensor.")
+    if weights.dtype != torch.bfloat16:
+        raise ValueError("weights must be a bfloat16 tensor.")
+    if logits.dtype != torch.float32:
+        raise ValueError("logits must be a float32 tensor.")
+    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
+        raise ValueError("q_scale and k_scale must be float32 tensors.")
+    head, dim = q.shape[-2], q.shape[-1]
+    if head not in heads:
+        raise ValueError(f"Unsupported head size: {head}. Sparse index op currently only "
+                         f"supports a head number of {' or '.join(map(str, heads))}.")
+    if dim != 128 or kv.shape[-1] != 128:
+        raise ValueError("dim must be 128, as we precompute scale inner kernel")
+    device = q.device
+    if any(t.device != device for t in (q_scale, kv, k_scale, weights, logits)):
+        raise ValueError("sparse_index inputs must be on the same device")
+    _require_cuda("sparse_index", q)
+    for t in (q, q_scale, kv, k_scale, weights, logits):
+        if not t.is_contiguous():
+            raise ValueError("sparse_index inputs must be contiguous")
+
+
+def sparse_index(q: torch.Tensor, q_scale: torch.Tensor, kv: torch.Tensor, k_scale: torch.Tensor,
+                 weights: torch.Tensor, logits: torch.Tensor, cur_pos: int,
+                 profile_logs: torch.Tensor | None = None, compute_kernel_type: str = "fp8", *,
+                 model_arch: str = "deepseek_v3_2") -> None:
+    """logits[t, l] = sum_h weights[t,h] * ReLU(q[t,h] . kv[l]) (dequantised), for the
+    token at position ``cur_pos + t`` and keys l <= cur_pos + t; -inf for later keys.
+
+    q [.., M, H, 128] e4m3fn; q_scale [M] or [M, H]; kv [L, 128] e4m3fn; k_scale [L];
+    weights [M, H] bf16; logits [M, ld] fp32 (ld >= L; columns >= L are not written).
+    """
+    if compute_kernel_type != "fp8":
+        raise ValueError(f"unsupported compute_kernel_type {compute_kernel_type!r}")
+    _check(q, q_scale, kv, k_scale, weights, logits)
+    H = q.shape[-2]
+    M = q.numel() // (H * 128)
+    L = kv.numel() // 128
+    if weights.numel() != M * H:
+        raise ValueError("weights must be [M, H]")
+    per_head = q_scale.numel() == M * H and H > 1
+    if not per_head and q_scale.numel() != M:
+        raise ValueError("q_scale must be [M] or [M, H]")
+    if k_scale.numel() != L:
+        raise ValueError("k_scale must be [L]")
+    ld = logits.shape[-1]
+    if logits.numel() != M * ld or ld < L:
+        raise ValueError("logits must be [M, ld] with ld >= L")
+    _lib.call("tl_indexer_fp8_scores", q.data_ptr(), q_scale.data_ptr(), int(per_head), kv.data_ptr(),
+              k_scale.data_ptr(), weights.data_ptr(), logits.data_ptr(), M, H, L, ld, int(cur_pos), _stream(q))
+
+
+def sparse_index_topk(q: torch.Tensor, q_scale: torch.Tensor, kv: torch.Tensor,
+                      k_scale: torch.Tensor, weights: torch.Tensor, logits: torch.Tensor,
+                      indices: torch.Tensor, cur_pos: int,
+                      profile_logs: torch.Tensor | None = None) -> None:
+    """``sparse_index`` followed by the exact top-k of every token's visible keys
+    (token t sees keys 0 .. cur_pos + t).  indices int32 [M, k] (k = 2048 in DSA) receives
+    the selected key positions in ascending order, -1 past the visible count."""
+    if q.shape[-2] != 64:
+        raise ValueError(f"Unsupported head size: {q.shape[-2]}. Sparse index topk fused op "
+                         "supports head number of 64 (DSV3.2).")
+    sparse_index(q, q_scale, kv, k_scale, weights, logits, cur_pos, profile_logs)
+    M = logits.numel() // logits.shape[-1]
+    if indices.dtype != torch.int32 or indices.numel() % M:
+        raise ValueError("indices must be an int32 [M, k] tensor")
+    k = indices.numel() // M
+    topk_rows(logits.reshape(M, -1), valid_base=int(cur_pos), k=k, out=indices.reshape(M, k))
