@@ -4,19 +4,20 @@
 // every scale is positive (the form of sparse_index_op, ops/sparse_index.py:11-69, on the
 // fp8 cache layout of pd_vllm/profiles/mla_nsa.py:211-228).
 //
-// gfx950 mapping: the M*H query rows form M*H/16 tiles of 16 rows x 128 dims, held in
-// registers for the whole kernel (A operand); each wave streams its own range of 16-key
-// tiles (B operand, 2 KB contiguous each, one tile prefetched ahead) through the native
-// fp8 MFMA v_mfma_f32_16x16x128_f8f6f4 -- one MFMA is a whole 128-long dot product for
-// 16 heads x 16 keys.  Epilogue per MFMA: ReLU and the head weight (2 VALU ops per
-// element); the head sum over a lane's 4 heads and a token's tiles stays in registers,
-// and the 4 lane groups are combined with two cross-lane exchanges.
+// gfx950 mapping: the M*H query rows form M*H/16 tiles of 16 rows x 128 dims, staged
+// once per workgroup through LDS and held in registers for the whole kernel (A operand);
+// each wave streams its own range of 16-key tiles (B operand, 2 KB contiguous each, one
+// tile prefetched ahead) through the native fp8 MFMA v_mfma_f32_16x16x128_f8f6f4 -- one
+// MFMA is a whole 128-long dot product for 16 heads x 16 keys.  Epilogue per MFMA: ReLU
+// and the head weight (2 VALU ops per element, weights read from LDS); the head sum over
+// a lane's 4 heads and a token's tiles stays in registers, and the 4 lane groups are
+// combined with v_permlane32_swap / v_permlane16_swap.
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
 namespace tl {
 
-constexpr int kIdxWaves = 4;
+constexpr int kIdxWaves = 8;
 
 template <int M, int H>
 __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
@@ -29,36 +30,35 @@ __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
   const int wave_global = blockIdx.x * kIdxWaves + (threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int t_begin = wave_global * tiles_per_wave;
-  if (t_begin >= n_tiles) return;
-  const int t_end = min(n_tiles, t_begin + tiles_per_wave);
-
-  // query tiles (A operands) and folded head weights w[t,h] * q_s for this lane's rows
-  v8i qa[QT];
-  float wq[QT][4];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    qa[qt] = load_kblock(q + static_cast<size_t>(qt * 16 + r) * kBlock, g);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = qt * 16 + 4 * g + j;  // flattened (token, head)
-      const int tok = row / H;
-      const float sq = q_s_per_head ? q_s[row] : q_s[tok];
-      wq[qt][j] = bf16_to_f32(w[row]) * sq;
-    }
-  }
 
   auto load_keys = [&](int tile) -> v8i {
     const int key = tile * 16 + r;
     return key < L ? load_kblock_stream(k + static_cast<size_t>(key) * kBlock, g) : zero_v8i();
   };
+  // the first key tile is in flight while the workgroup stages the queries
+  v8i kb_next = t_begin < n_tiles ? load_keys(t_begin) : zero_v8i();
 
-  v8i kb_next = load_keys(t_begin);
+  // stage the queries and the folded head weights w[t,h] * q_s once per workgroup
+  __shared__ __attribute__((aligned(16))) uint8_t q_lds[QT * 16 * kBlock];
+  __shared__ __attribute__((aligned(16))) float wq_lds[QT * 16];
+  for (int i = threadIdx.x; i < QT * 16 * kBlock / 16; i += kIdxWaves * 64)
+    reinterpret_cast<uint4*>(q_lds)[i] = reinterpret_cast<const uint4*>(q)[i];
+  for (int row = threadIdx.x; row < QT * 16; row += kIdxWaves * 64)
+    wq_lds[row] = bf16_to_f32(w[row]) * (q_s_per_head ? q_s[row] : q_s[row / H]);
+  __syncthreads();
+  if (t_begin >= n_tiles) return;
+  const int t_end = min(n_tiles, t_begin + tiles_per_wave);
+
+  v8i qa[QT];  // query tiles (A operands), resident for the whole kernel
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) qa[qt] = load_kblock(q_lds + (qt * 16 + r) * kBlock, g);
+
   for (int tile = t_begin; tile < t_end; ++tile) {
     const v8i kbv = kb_next;
     if (tile + 1 < t_end) kb_next = load_keys(tile + 1);
     const int key = tile * 16 + r;
     const float ks = key < L ? k_s[key] : 0.f;
-    float score[M];
+    float part[M];
 #pragma unroll
     for (int t = 0; t < M; ++t) {
       float acc = 0.f;
@@ -66,13 +66,23 @@ __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
       for (int i = 0; i < TPT; ++i) {
         const int qt = t * TPT + i;
         const v4f c = mfma_16x16x128_fp8(qa[qt], kbv);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc = __builtin_fmaf(fmaxf(c[j], 0.f), wq[qt][j], acc);
+        const float4 wq = *reinterpret_cast<const float4*>(wq_lds + qt * 16 + 4 * g);
+        acc = __builtin_fmaf(fmaxf(c[0], 0.f), wq.x, acc);
+        acc = __builtin_fmaf(fmaxf(c[1], 0.f), wq.y, acc);
+        acc = __builtin_fmaf(fmaxf(c[2], 0.f), wq.z, acc);
+        acc = __builtin_fmaf(fmaxf(c[3], 0.f), wq.w, acc);
       }
-      // lanes r, r+16, r+32, r+48 hold the 4 partial head sums of key r
-      acc += __shfl_xor(acc, 16);
-      acc += __shfl_xor(acc, 32);
-      score[t] = acc * ks;
+      part[t] = acc;
+    }
+    // lanes r, r+16, r+32, r+48 hold the 4 partial head sums of key r: sum them with
+    // the gfx950 lane-swap instructions (VALU, no LDS round trip)
+    float score[M];
+#pragma unroll
+    for (int t = 0; t < M; ++t) {
+      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[t]), __float_as_uint(part[t]), false, false);
+      const float y = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+      score[t] = (__uint_as_float(s16[0]) + __uint_as_float(s16[1])) * ks;
     }
     // lane group g stores tokens g, g+4, ...: a 64-byte row segment per token
 #pragma unroll
@@ -130,7 +140,8 @@ extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_
     const int64_t n = (L - visible) * M;
     hipLaunchKernelGGL(fill_masked_kernel, dim3(cdiv(n, 256)), dim3(256), 0, st, logits, (int)M, ld, visible, L);
   }
-  // 4 key tiles (64 keys, 8 KB) per wave at 128K keys: 2048 waves, 2 per SIMD
+  // 4 key tiles (64 keys, 8 KB) per wave at 128K keys: 2048 waves = 2 per SIMD, one
+  // 8-wave workgroup per CU (the kernel uses ~244 VGPRs at M*H = 256)
   const int tpw = static_cast<int>(cdiv(n_tiles, 2048) < 2 ? 2 : cdiv(n_tiles, 2048));
   const int waves = static_cast<int>(cdiv(n_tiles, tpw));
   const dim3 grid(static_cast<unsigned>(cdiv(waves, kIdxWaves)));

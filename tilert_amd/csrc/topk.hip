@@ -1,53 +1,59 @@
 // Exact per-row top-k by radix select (the contract of topk_accurate_op, ops/topk.py:62-109;
-// its golden is torch.topk, :128-143).
+// its golden is torch.topk, :128-143), as ONE kernel.
 //
-// Scores are mapped to order-preserving 32-bit keys (larger score = larger key).  Three
-// passes over the row find the k-th largest key T digit by digit (11, 11, 10 bits): each
-// pass builds per-workgroup LDS histograms of the next digit among the elements that
-// match the prefix found so far, merges them into a per-row global histogram with
-// agent-scope atomics, and the last workgroup of the row to finish picks the digit.  A
-// count pass and a write pass then emit, in ascending index order, every element with
-// key > T plus the lowest-index elements with key == T until k are taken -- so the output
-// set is exact and deterministic, ties included.
+// Scores map to order-preserving 32-bit keys (larger score = larger key).  A row is cut
+// into 16K-column chunks, one 1024-thread workgroup each, which load their keys once and
+// keep them in registers.  Three passes find the k-th largest key T digit by digit (11,
+// 11, 10 bits): each workgroup histograms its chunk's keys that match the prefix found
+// so far in LDS and publishes the histogram (agent-scope stores); the row's workgroups
+// meet at a per-row barrier; then EVERY workgroup merges all partials (so no second
+// barrier is needed), picks the same digit, and accumulates how many elements of the
+// chunks before its own are now known to be > T (and, after the last pass, == T).  It
+// then writes its selected columns -- every key > T plus the lowest-column keys == T
+// until k are taken -- in ascending column order at their global rank.  The set is exact
+// and deterministic, ties included.
+//
+// The per-row barrier needs the row's workgroups co-resident: the launch is at most one
+// workgroup per CU (<= 256 workgroups, checked on the host) and the kernel is the only
+// work on its stream; the wait is bounded (about a second) so a wave can never hang.
 //
 // Rows are the topk_accurate samples: row i considers columns [0, valid_base + 1 + i).
+#include <mutex>
+
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
 namespace tl {
 
-constexpr int kTopkThreads = 256;
-constexpr int kChunk = 4096;     // elements per workgroup per row
-constexpr int kBins = 2048;      // max digit width 11 bits
+constexpr int kTkThreads = 1024;
+constexpr int kTkPerThread = 16;                      // 4 float4 loads in flight per thread
+constexpr int kTkChunk = kTkThreads * kTkPerThread;   // 16384 columns per workgroup
+constexpr int kBins = 2048;                           // widest digit: 11 bits
 constexpr int kMaxK = 8192;
+// every workgroup keeps all chunks' partial histograms of a pass in LDS: 16 x 8 KB
+constexpr int kMaxChunks = 16;
+constexpr int kMaxCols = kMaxChunks * kTkChunk;  // 262144
+constexpr int kMaxGroups = 256;                  // one workgroup per CU at most
+constexpr uint32_t kSpinLimit = 1u << 22;        // x s_sleep(8): ~1 s
 
-struct RowState {
-  uint32_t prefix;  // key bits decided so far (right-aligned)
-  int32_t k_rem;    // still to take among elements matching the prefix
-  uint32_t pad[2];
-};
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Workspace layout (bytes): [hist rows*kBins u32][counter rows u32][state rows RowState]
-// [counts rows*chunks*2 u32]
 struct TopkWs {
-  uint32_t* hist;
-  uint32_t* counter;
-  RowState* state;
-  uint32_t* counts;
+  uint32_t* part;     // [rows][3 passes][chunks][kBins] partial histograms
+  uint32_t* arrive;   // [rows] barrier arrivals, zero between calls
+  uint32_t* leave;    // [rows] finished workgroups, zero between calls
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-__host__ __device__ inline TopkWs carve(void* base, int64_t rows, int64_t chunks) {
+__host__ __device__ inline TopkWs carve(void* base, int64_t rows) {
   char* p = static_cast<char*>(base);
   TopkWs w;
-  w.hist = reinterpret_cast<uint32_t*>(p);
-  p += align256(rows * kBins * sizeof(uint32_t));
-  w.counter = reinterpret_cast<uint32_t*>(p);
+  w.arrive = reinterpret_cast<uint32_t*>(p);
   p += align256(rows * sizeof(uint32_t));
-  w.state = reinterpret_cast<RowState*>(p);
-  p += align256(rows * sizeof(RowState));
-  w.counts = reinterpret_cast<uint32_t*>(p);
+  w.leave = reinterpret_cast<uint32_t*>(p);
+  p += align256(rows * sizeof(uint32_t));
+  w.part = reinterpret_cast<uint32_t*>(p);
   return w;
 }
 
@@ -63,183 +69,198 @@ __device__ inline int row_valid(int row, int64_t valid_base, int64_t ld) {
   return static_cast<int>(n);
 }
 
-// pass 0: bits 31..21, pass 1: 20..10, pass 2: 9..0
-__device__ inline int pass_shift(int p) { return p == 0 ? 21 : (p == 1 ? 10 : 0); }
-__device__ inline int pass_width(int p) { return p == 2 ? 10 : 11; }
+// The 16 keys of this thread's contiguous columns [c0, c0 + 16); invalid ones flagged.
+__device__ inline void load_keys(const float* __restrict__ src, int64_t c0, int n, uint32_t (&key)[kTkPerThread],
+                                 uint32_t& valid_mask) {
+  valid_mask = 0;
+  if (c0 + kTkPerThread <= n) {
+    f32x4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + c0 + 4 * i);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) key[4 * i + j] = order_key(v[i][j]);
+    valid_mask = 0xffffu;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kTkPerThread; ++i) {
+      const bool ok = c0 + i < n;
+      key[i] = ok ? order_key(src[c0 + i]) : 0u;
+      valid_mask |= ok ? (1u << i) : 0u;
+    }
+  }
+}
 
-__global__ __launch_bounds__(kTopkThreads) void radix_pass_kernel(const float* __restrict__ logits, int64_t ld,
-                                                                  int64_t valid_base, int k, TopkWs ws, int pass) {
+// Block-wide exclusive prefix sum over the 1024 threads (returns the block total too).
+__device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s_waves, uint32_t& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_waves[wave] = x;
+  __syncthreads();
+  uint32_t before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kTkThreads / 64; ++w) {
+    const uint32_t s = s_waves[w];
+    before += w < wave ? s : 0u;
+    total += s;
+  }
+  __syncthreads();
+  return before + x - v;
+}
+
+__device__ inline uint32_t block_sum(uint32_t v, uint32_t* s_waves) {
+  uint32_t total;
+  block_excl_scan(v, s_waves, total);
+  return total;
+}
+
+__global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restrict__ logits, int64_t ld,
+                                                          int64_t valid_base, int k, TopkWs ws,
+                                                          int32_t* __restrict__ out) {
+  extern __shared__ uint32_t plds[];  // [chunks][nb]: every chunk's partial of this pass
   __shared__ uint32_t h[kBins];
-  __shared__ uint32_t part[kTopkThreads];
-  __shared__ int last;
+  __shared__ uint32_t s_waves[kTkThreads / 64];
+  __shared__ uint32_t s_digit, s_above;
   const int row = blockIdx.y;
-  const int n = row_valid(row, valid_base, ld);
-  if (n <= k) return;  // the whole row is selected
-  const int shift = pass_shift(pass), width = pass_width(pass);
-  const uint32_t nb = 1u << width;
-  uint32_t prefix = 0;
-  int k_rem = k;
-  if (pass > 0) {
-    prefix = ws.state[row].prefix;
-    k_rem = ws.state[row].k_rem;
-  }
-  for (uint32_t b = threadIdx.x; b < nb; b += kTopkThreads) h[b] = 0;
-  __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
-  const float* src = logits + static_cast<int64_t>(row) * ld;
-  for (int i = threadIdx.x; i < kChunk; i += kTopkThreads) {
-    const int64_t c = base + i;
-    if (c < n) {
-      const uint32_t key = order_key(src[c]);
-      const bool match = pass == 0 || (key >> (shift + width)) == prefix;
-      if (match) atomicAdd(&h[(key >> shift) & (nb - 1)], 1u);
-    }
-  }
-  __syncthreads();
-  uint32_t* gh = ws.hist + static_cast<size_t>(row) * kBins;
-  for (uint32_t b = threadIdx.x; b < nb; b += kTopkThreads)
-    if (h[b]) __hip_atomic_fetch_add(&gh[b], h[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t chunks = gridDim.x;
-    const uint32_t prev = __hip_atomic_fetch_add(&ws.counter[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = prev == chunks - 1;
-  }
-  __syncthreads();
-  if (!last) return;
-
-  // ---- last workgroup of the row: pick the digit holding the k_rem-th largest key
-  for (uint32_t b = threadIdx.x; b < nb; b += kTopkThreads) {
-    h[b] = __hip_atomic_load(&gh[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&gh[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  // thread j owns the bins [nb - (j+1)*per, nb - j*per) (descending digit order)
-  const uint32_t per = nb / kTopkThreads;
-  const uint32_t hi = nb - threadIdx.x * per;
-  uint32_t s = 0;
-  for (uint32_t b = hi - per; b < hi; ++b) s += h[b];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t above = 0;  // elements with a larger digit
-    int j = 0;
-    for (; j < kTopkThreads; ++j) {
-      if (above + part[j] >= static_cast<uint32_t>(k_rem)) break;
-      above += part[j];
-    }
-    const uint32_t top = nb - j * per;
-    uint32_t d = top - 1;
-    for (;; --d) {
-      if (above + h[d] >= static_cast<uint32_t>(k_rem)) break;
-      above += h[d];
-    }
-    ws.state[row].prefix = (prefix << width) | d;
-    ws.state[row].k_rem = k_rem - static_cast<int>(above);
-    __hip_atomic_store(&ws.counter[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// per chunk: number of keys > T and == T
-__global__ __launch_bounds__(kTopkThreads) void count_kernel(const float* __restrict__ logits, int64_t ld,
-                                                             int64_t valid_base, int k, TopkWs ws) {
-  __shared__ uint32_t sgt, seq;
-  const int row = blockIdx.y;
-  const int n = row_valid(row, valid_base, ld);
-  if (n <= k) return;
-  if (threadIdx.x == 0) { sgt = 0; seq = 0; }
-  __syncthreads();
-  const uint32_t T = ws.state[row].prefix;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
-  const float* src = logits + static_cast<int64_t>(row) * ld;
-  uint32_t gt = 0, eq = 0;
-  for (int i = threadIdx.x; i < kChunk; i += kTopkThreads) {
-    const int64_t c = base + i;
-    if (c < n) {
-      const uint32_t key = order_key(src[c]);
-      gt += key > T;
-      eq += key == T;
-    }
-  }
-  atomicAdd(&sgt, gt);
-  atomicAdd(&seq, eq);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* cnt = ws.counts + (static_cast<size_t>(row) * gridDim.x + blockIdx.x) * 2;
-    cnt[0] = sgt;
-    cnt[1] = seq;
-  }
-}
-
-// Emit the selected indices of this chunk in ascending order at their global rank.
-__global__ __launch_bounds__(kTopkThreads) void write_kernel(const float* __restrict__ logits, int64_t ld,
-                                                             int64_t valid_base, int k, TopkWs ws,
-                                                             int32_t* __restrict__ out) {
-  __shared__ uint32_t wsel[kTopkThreads / 64], weq[kTopkThreads / 64];
-  __shared__ uint32_t s_sel_base, s_eq_base;
-  const int row = blockIdx.y;
+  const int chunks = gridDim.x, chunk = blockIdx.x;
   const int n = row_valid(row, valid_base, ld);
   int32_t* o = out + static_cast<int64_t>(row) * k;
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
-  if (n <= k) {  // everything valid is selected; pad with -1
-    for (int i = threadIdx.x; i < kChunk; i += kTopkThreads) {
-      const int64_t c = base + i;
-      if (c < k) o[c] = c < n ? static_cast<int32_t>(c) : -1;
-    }
-    if (blockIdx.x == 0)  // k may exceed the chunked range
-      for (int64_t c = static_cast<int64_t>(gridDim.x) * kChunk + threadIdx.x; c < k; c += kTopkThreads)
-        o[c] = c < n ? static_cast<int32_t>(c) : -1;
+  if (n <= k) {  // every valid column, then -1 padding (no barrier: the whole row exits)
+    const int64_t base = static_cast<int64_t>(chunk) * kTkChunk;
+    for (int64_t c = base + threadIdx.x; c < base + kTkChunk && c < k; c += kTkThreads)
+      o[c] = c < n ? static_cast<int32_t>(c) : -1;
     return;
   }
-  const uint32_t T = ws.state[row].prefix;
-  const uint32_t need_eq = static_cast<uint32_t>(ws.state[row].k_rem);
-  if (threadIdx.x == 0) {
-    uint32_t gt = 0, eq = 0;
-    const uint32_t* cnt = ws.counts + static_cast<size_t>(row) * gridDim.x * 2;
-    for (uint32_t c = 0; c < blockIdx.x; ++c) {
-      gt += cnt[2 * c];
-      eq += cnt[2 * c + 1];
-    }
-    s_sel_base = gt + (eq < need_eq ? eq : need_eq);
-    s_eq_base = eq;
-  }
-  __syncthreads();
+
   const float* src = logits + static_cast<int64_t>(row) * ld;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int i0 = 0; i0 < kChunk; i0 += kTopkThreads) {
-    const int64_t c = base + i0 + threadIdx.x;
-    uint32_t key = 0;
-    bool valid = c < n;
-    if (valid) key = order_key(src[c]);
-    const bool is_eq = valid && key == T;
-    const bool is_gt = valid && key > T;
-    // rank of this element among the chunk's equals so far (ascending index)
-    const uint64_t eq_mask = __ballot(is_eq);
-    const uint32_t eq_lane = __builtin_popcountll(eq_mask & ((1ull << lane) - 1));
-    if (lane == 0) weq[wave] = __builtin_popcountll(eq_mask);
+  const int64_t c0 = static_cast<int64_t>(chunk) * kTkChunk + static_cast<int64_t>(threadIdx.x) * kTkPerThread;
+  uint32_t key[kTkPerThread], vm;
+  load_keys(src, c0, n, key, vm);
+
+  uint32_t prefix = 0;
+  int k_rem = k;
+  uint32_t gt_before = 0, eq_before = 0;  // over the chunks preceding this one
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const int width = pass == 2 ? 10 : 11;
+    const uint32_t nb = 1u << width;
+    for (uint32_t b = threadIdx.x; b < nb; b += kTkThreads) h[b] = 0;
     __syncthreads();
-    uint32_t eq_before_wave = 0;
-    for (int w = 0; w < wave; ++w) eq_before_wave += weq[w];
-    const uint32_t eq_rank = s_eq_base + eq_before_wave + eq_lane;
-    const bool sel = is_gt || (is_eq && eq_rank < need_eq);
-    const uint64_t sel_mask = __ballot(sel);
-    const uint32_t sel_lane = __builtin_popcountll(sel_mask & ((1ull << lane) - 1));
-    if (lane == 0) wsel[wave] = __builtin_popcountll(sel_mask);
-    __syncthreads();
-    uint32_t sel_before_wave = 0, sel_total = 0, eq_total = 0;
-    for (int w = 0; w < kTopkThreads / 64; ++w) {
-      if (w < wave) sel_before_wave += wsel[w];
-      sel_total += wsel[w];
-      eq_total += weq[w];
+#pragma unroll
+    for (int i = 0; i < kTkPerThread; ++i) {
+      const bool match = ((vm >> i) & 1u) && (pass == 0 || (key[i] >> (shift + width)) == prefix);
+      if (match) atomicAdd(&h[(key[i] >> shift) & (nb - 1)], 1u);
     }
-    if (sel) o[s_sel_base + sel_before_wave + sel_lane] = static_cast<int32_t>(c);
     __syncthreads();
+    uint32_t* part = ws.part + (static_cast<size_t>(row) * 3 + pass) * chunks * kBins;
+    for (uint32_t b = threadIdx.x; b < nb; b += kTkThreads)
+      __hip_atomic_store(&part[static_cast<size_t>(chunk) * kBins + b], h[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // ---- per-row barrier (bounded wait)
     if (threadIdx.x == 0) {
-      s_sel_base += sel_total;
-      s_eq_base += eq_total;
+      __hip_atomic_fetch_add(&ws.arrive[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t target = static_cast<uint32_t>(chunks) * (pass + 1);
+      for (uint32_t it = 0; it < kSpinLimit; ++it) {
+        if (__hip_atomic_load(&ws.arrive[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+        __builtin_amdgcn_s_sleep(8);
+      }
     }
     __syncthreads();
+    // ---- merge every chunk's partial (batched agent-scope loads) into LDS
+    for (uint32_t b = threadIdx.x; b < nb; b += kTkThreads) {
+      uint32_t s = 0;
+      for (int cg = 0; cg < chunks; cg += 16) {
+        uint32_t v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int c = cg + u < chunks ? cg + u : chunks - 1;
+          v[u] = __hip_atomic_load(&part[static_cast<size_t>(c) * kBins + b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (cg + u < chunks) {
+            plds[(cg + u) * nb + b] = v[u];
+            s += v[u];
+          }
+      }
+      h[b] = s;
+    }
+    __syncthreads();
+    // ---- the digit holding the k_rem-th largest: thread j owns digits
+    // [nb - (j+1)*per, nb - j*per), i.e. descending order across threads
+    const uint32_t per = nb / kTkThreads;  // 2 or 1
+    const uint32_t hi = nb - threadIdx.x * per;
+    uint32_t own = 0;
+    for (uint32_t b = hi - per; b < hi; ++b) own += h[b];
+    uint32_t total;
+    const uint32_t above_me = block_excl_scan(own, s_waves, total);
+    if (above_me < static_cast<uint32_t>(k_rem) && above_me + own >= static_cast<uint32_t>(k_rem)) {
+      uint32_t above = above_me;
+      uint32_t d = hi - 1;
+      for (;; --d) {
+        if (above + h[d] >= static_cast<uint32_t>(k_rem)) break;
+        above += h[d];
+      }
+      s_digit = d;
+      s_above = above;
+    }
+    __syncthreads();
+    const uint32_t d = s_digit;
+    // elements of the preceding chunks now known to be > T (digit above d)
+    uint32_t g = 0;
+    for (int i = threadIdx.x; i < chunk * static_cast<int>(nb); i += kTkThreads) {
+      const uint32_t b = static_cast<uint32_t>(i) & (nb - 1);
+      g += b > d ? plds[i] : 0u;
+    }
+    gt_before += block_sum(g, s_waves);
+    if (pass == 2) {
+      uint32_t e = 0;
+      for (int c = threadIdx.x; c < chunk; c += kTkThreads) e += plds[c * nb + d];
+      eq_before = block_sum(e, s_waves);
+    }
+    prefix = (prefix << width) | d;
+    k_rem -= static_cast<int>(s_above);
+    __syncthreads();
+  }
+
+  // ---- emit this chunk's selected columns in ascending order at their global rank
+  const uint32_t T = prefix;
+  const uint32_t need_eq = static_cast<uint32_t>(k_rem);
+  uint32_t n_eq = 0;
+#pragma unroll
+  for (int i = 0; i < kTkPerThread; ++i) n_eq += ((vm >> i) & 1u) && key[i] == T;
+  uint32_t tot;
+  uint32_t eq_rank = eq_before + block_excl_scan(n_eq, s_waves, tot);
+  uint32_t sel_bits = 0;
+#pragma unroll
+  for (int i = 0; i < kTkPerThread; ++i) {
+    const bool valid = (vm >> i) & 1u;
+    const bool eq = valid && key[i] == T;
+    const bool sel = (valid && key[i] > T) || (eq && eq_rank < need_eq);
+    eq_rank += eq;
+    sel_bits |= sel ? (1u << i) : 0u;
+  }
+  const uint32_t sel_base = gt_before + (eq_before < need_eq ? eq_before : need_eq);
+  uint32_t pos = sel_base + block_excl_scan(__builtin_popcount(sel_bits), s_waves, tot);
+#pragma unroll
+  for (int i = 0; i < kTkPerThread; ++i)
+    if ((sel_bits >> i) & 1u) o[pos++] = static_cast<int32_t>(c0 + i);
+
+  // ---- the last workgroup of the row out re-arms the barrier counters
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&ws.leave[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == static_cast<uint32_t>(chunks - 1)) {
+      __hip_atomic_store(&ws.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ws.leave[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -247,31 +268,37 @@ __global__ __launch_bounds__(kTopkThreads) void write_kernel(const float* __rest
 
 using namespace tl;
 
-static int64_t topk_chunks(int64_t ld) { return cdiv(ld, kChunk); }
+static int64_t topk_chunks(int64_t ld) { return cdiv(ld, kTkChunk); }
 
 extern "C" size_t tl_topk_workspace_bytes(int64_t rows, int64_t ld, int64_t k) {
   (void)k;
   if (rows <= 0 || ld <= 0) return 0;
   const int64_t chunks = topk_chunks(ld);
-  return align256(rows * kBins * 4) + align256(rows * 4) + align256(rows * sizeof(RowState)) +
-         align256(rows * chunks * 2 * 4);
+  return 2 * align256(rows * 4) + align256(static_cast<size_t>(rows) * 3 * chunks * kBins * 4);
 }
 
 extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64_t valid_base, int64_t k,
                             int32_t* out, void* workspace, size_t workspace_bytes, void* stream) {
   if (rows <= 0 || ld <= 0) { set_error("topk: empty input (rows=%lld ld=%lld)", (long long)rows, (long long)ld); return kErrArg; }
   if (k < 1 || k > kMaxK) { set_error("topk: k=%lld must be in [1, %d]", (long long)k, kMaxK); return kErrUnsupported; }
-  if (rows > 65535 || ld > (1ll << 30)) { set_error("topk: too many rows or columns"); return kErrArg; }
+  if (ld > kMaxCols) { set_error("topk: ld=%lld > %d columns is not supported", (long long)ld, kMaxCols); return kErrUnsupported; }
+  if (ld % 4) { set_error("topk: ld=%lld must be a multiple of 4 (16-byte rows)", (long long)ld); return kErrArg; }
+  const int64_t chunks = topk_chunks(ld);
+  if (rows * chunks > kMaxGroups) { set_error("topk: rows * ceil(ld/16384) = %lld exceeds %d co-resident workgroups", (long long)(rows * chunks), kMaxGroups); return kErrUnsupported; }
   if (!logits || !out) { set_error("topk: null pointer"); return kErrArg; }
+  if (reinterpret_cast<uintptr_t>(logits) & 15) { set_error("topk: logits must be 16-byte aligned"); return kErrArg; }
   const size_t need = tl_topk_workspace_bytes(rows, ld, k);
   if (!workspace || workspace_bytes < need) { set_error("topk: workspace of %zu bytes required (got %zu)", need, workspace_bytes); return kErrArg; }
-  const int64_t chunks = topk_chunks(ld);
-  const TopkWs ws = carve(workspace, rows, chunks);
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(rows));
-  for (int p = 0; p < 3; ++p)
-    hipLaunchKernelGGL(radix_pass_kernel, grid, dim3(kTopkThreads), 0, st, logits, ld, valid_base, (int)k, ws, p);
-  hipLaunchKernelGGL(count_kernel, grid, dim3(kTopkThreads), 0, st, logits, ld, valid_base, (int)k, ws);
-  hipLaunchKernelGGL(write_kernel, grid, dim3(kTopkThreads), 0, st, logits, ld, valid_base, (int)k, ws, out);
+  const TopkWs ws = carve(workspace, rows);
+  const size_t lds = static_cast<size_t>(chunks) * kBins * sizeof(uint32_t);
+  static std::once_flag once;  // allow the >64 KB dynamic LDS gfx950 offers (160 KB per CU)
+  static hipError_t attr_rc = hipSuccess;
+  std::call_once(once, [] {
+    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(topk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  kMaxChunks * kBins * static_cast<int>(sizeof(uint32_t)));
+  });
+  if (attr_rc != hipSuccess) { set_error("topk: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc)); return kErrHip; }
+  hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), dim3(kTkThreads),
+                     lds, (hipStream_t)stream, logits, ld, valid_base, (int)k, ws, out);
   return check_launch("topk");
 }
