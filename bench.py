@@ -105,6 +105,20 @@ def cpu_baseline_linear(torch, q, s, xq, xs, M, N, K):
     return us, us_deq, cores
 
 
+def measured_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE +
+    WRITE_SIZE, each scaled by a plain copy's reading), or None when absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -223,6 +237,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--extras", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy 10 times (scales rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU's share of the layout (TP/EP shard shapes); "
@@ -236,6 +252,15 @@ def main() -> int:
         print("bench.py: no GPU visible", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "calls": 10}))
+        return 0
     M, N, Kd = 4, 18432, 7168
     us, ws, x, xq, xs, out = bench_gemm(torch, M, N, Kd, args.steps, args.warmup, 5, dev)
     nbytes = gemm_bytes(M, N, Kd)
@@ -259,7 +284,9 @@ def main() -> int:
                    "weight_layout": "mfma-fragment-packed", "weight_copies_rotated": 5,
                    "timing": "HIP graph of K calls, HIP events around the replay"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic("fp8_gemm_M4_7168x18432.md"),
+                     "traffic_source": "profiles/fp8_gemm_M4_7168x18432.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                      "kernel": "tl::fp8_gemm_kernel<1, 8, true>", "bytes_per_call": nbytes},
     }
     if not args.no_cpu_baseline:

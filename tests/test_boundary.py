@@ -1,0 +1,83 @@
+"""The C ABI boundary: the library loads, exports every entry point include/tilert_amd.h
+declares, and the Python wrappers fail loudly (no CPU fallback).  CPU only."""
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "tilert_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(tl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_symbols()
+    for n in ("tl_act_quant", "tl_fp8_gemm", "tl_fp8_gemm_packed", "tl_moe_gate_up_swiglu",
+              "tl_moe_down_combine", "tl_indexer_fp8_scores", "tl_topk_rows", "tl_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from tilert_amd import _lib
+    lib = _lib.load()
+    missing = [n for n in declared_symbols() if getattr(lib, n, None) is None]
+    assert not missing, f"not exported: {missing}"
+    assert set(declared_symbols()) == set(_lib.SIGNATURES), "ctypes table out of sync with the header"
+    assert lib.tl_version().startswith(b"tilert_amd")
+
+
+def test_nm_shows_extern_c_exports():
+    out = subprocess.run(["nm", "-D", "--defined-only", str(ROOT / "tilert_amd" / "libtilert_amd.so")],
+                         capture_output=True, text=True).stdout
+    for n in declared_symbols():
+        assert re.search(rf"\bT {n}$", out, re.M), n
+
+
+def test_argument_errors_need_no_gpu():
+    """Status codes and messages come back through the ABI before any launch."""
+    from tilert_amd import _lib
+    lib = _lib.load()
+    assert lib.tl_fp8_gemm(None, None, None, None, None, 4, 100, 7168, None, 0, None) == 1
+    assert b"multiple of 16" in lib.tl_last_error()
+    assert lib.tl_fp8_gemm(None, None, None, None, None, 4, 128, 7168, None, 0, None) == 1
+    assert b"null pointer" in lib.tl_last_error()
+    assert lib.tl_fp8_gemm(None, None, None, None, None, 300, 128, 7168, None, 0, None) == 3
+    assert lib.tl_indexer_fp8_scores(None, None, 0, None, None, None, None, 4, 48, 10, 10, 0, None) == 3
+    assert lib.tl_topk_rows(None, 4, 131072, 0, 9000, None, None, 0, None) == 3
+    assert lib.tl_moe_gate_up_swiglu(None, None, None, None, 17, 8, 0, 32, 7168, 2048, None, None) == 3
+    assert lib.tl_act_quant(None, None, None, 4, 100, 128, 0, None) == 1
+    assert lib.tl_fp8_gemm_workspace_bytes(4, 576, 7168) > 0
+    assert lib.tl_fp8_gemm_workspace_bytes(4, 18432, 7168) == 0
+
+
+def test_wrappers_reject_cpu_tensors():
+    from tilert_amd import kernel as K
+    from tilert_amd.topk import topk_accurate
+    with pytest.raises(ValueError, match="GPU"):
+        K.act_quant(torch.zeros(2, 128, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        K.act_quant(torch.zeros(2, 128))  # wrong dtype
+    with pytest.raises(AssertionError):
+        K.act_quant(torch.zeros(2, 100, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="topk must be"):
+        topk_accurate(torch.zeros(1, 2, 8), 8, 100)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    code = ("import tilert_amd._lib as l\n"
+            "try:\n    l.load()\nexcept RuntimeError as e:\n    print('RAISED', e)\n")
+    env = {"TILERT_AMD_LIB": str(tmp_path / "nope.so"), "PATH": "/usr/bin:/bin"}
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, cwd=ROOT, env=env).stdout
+    assert "RAISED" in out and "no CPU fallback" in out
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr

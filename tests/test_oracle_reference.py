@@ -1,0 +1,160 @@
+"""Pins of the torch-CPU oracle (oracle/reference.py) against closed forms, invariants
+and fp64 brute force -- CPU only, each check chosen so a plausible slip (dropped scale,
+transposed operand, wrong index, sign error) fails it."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute, fp8
+from oracle import reference as ref
+from tilert_amd import synth
+
+
+# --------------------------------------------------------------------------- act_quant
+def test_act_quant_zero_group_scale_and_codes():
+    y, s = ref.act_quant(torch.zeros(2, 256, dtype=torch.bfloat16))
+    assert torch.all(s == torch.tensor(1e-4, dtype=torch.float32) * torch.tensor(1 / 448, dtype=torch.float32))
+    assert torch.all(y.view(torch.uint8) == 0)
+
+
+def test_act_quant_group_max_maps_to_448_and_scale_formula():
+    g = synth.gen(1)
+    x = synth.activations(8, 512, g)
+    y, s = ref.act_quant(x)
+    yf = y.float().reshape(8, 4, 128)
+    assert torch.all(yf.abs().amax(-1) == 448.0)
+    amax = x.float().reshape(8, 4, 128).abs().amax(-1)
+    assert torch.equal(s, amax * torch.tensor(1 / 448, dtype=torch.float32))
+
+
+def test_act_quant_matches_independent_numpy_codec():
+    g = synth.gen(2)
+    x = synth.activations(16, 1024, g) * 3
+    for mode in (0, 1, 2):
+        y, s = ref.act_quant(x, 128, mode)
+        xf = x.float().numpy().reshape(16, 8, 128)
+        q = fp8.encode(np.clip(xf / s.numpy()[..., None], -448, 448)).reshape(16, 1024)
+        assert np.array_equal(q, y.view(torch.uint8).numpy())
+
+
+def test_act_quant_ue8m0_is_smallest_power_of_two_covering_amax():
+    g = synth.gen(3)
+    x = synth.activations(4, 1024, g) * 10
+    _, s = ref.act_quant(x, 128, ref.SCALE_MODE_UE8M0)
+    amax = x.float().reshape(4, 8, 128).abs().amax(-1)
+    target = amax * torch.tensor(1 / 448, dtype=torch.float32)
+    e = torch.log2(s)
+    assert torch.all(e == torch.round(e))          # power of two
+    assert torch.all(s >= target) and torch.all(s / 2 < target)
+
+
+# ----------------------------------------------------------------- weights and GEMM
+def test_weight_quant_dequant_error_bound_and_partial_blocks():
+    w = synth.weight_fp32(300, 520, synth.gen(4))
+    q, s = ref.weight_quant(w)
+    assert s.shape == (3, 5)
+    d = ref.weight_dequant(q, s)
+    # e4m3 has 3 mantissa bits: relative rounding error <= 2^-4 for normals
+    blk = s.repeat_interleave(128, 0)[:300].repeat_interleave(128, 1)[:, :520]
+    assert torch.all((d - w).abs() <= blk * 448 * 2.0 ** -4 + blk * 2.0 ** -9)
+    zq, zs = ref.weight_quant(torch.zeros(128, 128))
+    assert zs.item() == 1.0 and torch.all(ref.weight_dequant(zq, zs) == 0)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 128), (3, 32, 256), (2, 130, 384)])
+def test_fp8_gemm_vs_fp64_brute_force(M, N, K):
+    g = synth.gen(M * N + K)
+    xq, xs = ref.act_quant(synth.activations(M, K, g))
+    wq, ws = ref.weight_quant(synth.weight_fp32(N, K, g))
+    want = brute.gemm_fp64(xq.view(torch.uint8).numpy(), xs.numpy(), wq.view(torch.uint8).numpy(), ws.numpy())
+    got = ref.fp8_gemm(xq, xs, wq, ws).double().numpy()
+    # the oracle rounds to bf16 once: within half a bf16 ulp (+ fp32 accumulation)
+    ulp = 2.0 ** (np.floor(np.log2(np.abs(want) + 1e-30)) - 7)
+    assert np.all(np.abs(got - want) <= 0.5 * ulp + 1e-6 * np.abs(want) + 1e-30)
+
+
+def test_fp8_gemm_scale_linearity_and_transpose_sensitivity():
+    g = synth.gen(5)
+    xq, xs = ref.act_quant(synth.activations(4, 512, g))
+    wq, ws = ref.weight_quant(synth.weight_fp32(256, 512, g))
+    base = ref.fp8_gemm(xq, xs, wq, ws)
+    assert torch.equal(ref.fp8_gemm(xq, xs, wq, ws * 2), base * 2)   # exact: power of two
+    assert torch.equal(ref.fp8_gemm(xq, xs * 4, wq, ws), base * 4)
+    ws2 = ws.clone()
+    ws2[1, 0] *= 2  # scale of rows 128..255, K block 0 only
+    out = ref.fp8_gemm(xq, xs, wq, ws2)
+    assert torch.equal(out[:, :128], base[:, :128]) and not torch.equal(out[:, 128:], base[:, 128:])
+
+
+# ----------------------------------------------------------------------------- MoE
+def _tiny_experts(E, D, I, g):
+    out = []
+    for (n, k) in ((I, D), (I, D), (D, I)):
+        q, s = zip(*[ref.weight_quant(synth.weight_fp32(n, k, g)) for _ in range(E)])
+        out += [torch.stack(q), torch.stack(s)]
+    return out
+
+
+def test_moe_vs_fp64_per_pair():
+    E, D, I, M = 4, 256, 128, 3
+    g = synth.gen(6)
+    gq, gs, uq, us, dq, ds = _tiny_experts(E, D, I, g)
+    x = synth.activations(M, D, g)
+    idx = torch.tensor([[0, 9, 2], [7, 8, 9], [2, 3, 11]], dtype=torch.int32)
+    w = torch.tensor([[0.5, 0.3, 0.2], [0.4, 0.4, 0.2], [0.1, 0.6, 0.3]])
+    y = ref.moe_forward(x, gq, gs, uq, us, dq, ds, idx, w, 0)
+    xd = x.double()
+    want = torch.zeros(M, D, dtype=torch.float64)
+    for t in range(M):
+        for j in range(3):
+            e = int(idx[t, j])
+            if e >= E:
+                continue
+            G = ref.weight_dequant(gq[e], gs[e]).to(torch.bfloat16).double()
+            U = ref.weight_dequant(uq[e], us[e]).to(torch.bfloat16).double()
+            Dw = ref.weight_dequant(dq[e], ds[e]).to(torch.bfloat16).double()
+            gg, uu = xd[t] @ G.T, xd[t] @ U.T
+            h = (gg / (1 + torch.exp(-gg)) * uu).to(torch.bfloat16).double()
+            want[t] += float(w[t, j]) * (h @ Dw.T)
+    assert torch.all(y[1] == 0)  # token 1 routes to no local expert
+    rel = (y.double() - want).norm() / want.norm()
+    assert rel < 3e-3
+
+
+# ------------------------------------------------------------------------- indexer
+@pytest.mark.parametrize("per_head", [False, True])
+def test_indexer_vs_fp64_brute_force(per_head):
+    M, H, L, cur = 2, 32, 40, 35
+    g = synth.gen(7)
+    q, qs, k, ks, w = synth.indexer_inputs(M, H, L, g)
+    if per_head:
+        qs = (torch.rand(M, H, generator=g) + 0.5) * qs[:, None]
+    got = ref.indexer_scores(q, qs, k, ks, w, cur).double().numpy()
+    want = brute.indexer_fp64(q.view(torch.uint8).numpy(), qs.numpy(), k.view(torch.uint8).numpy(),
+                              ks.numpy(), w.float().numpy(), cur)
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    assert np.abs(got[fin] - want[fin]).max() <= 1e-5 * np.abs(want[fin]).max()
+    assert np.isinf(got[0, cur + 1:]).all() and np.isfinite(got[1, : cur + 2]).all()
+
+
+def test_indexer_scale_factoring_identity():
+    """s_k scales scores linearly (positive scales commute with ReLU)."""
+    g = synth.gen(8)
+    q, qs, k, ks, w = synth.indexer_inputs(2, 64, 64, g)
+    a = ref.indexer_scores(q, qs, k, ks, w, 63)
+    b = ref.indexer_scores(q, qs, k, ks * 4, w, 63)
+    assert torch.allclose(b, a * 4, rtol=1e-6, atol=0)
+
+
+# --------------------------------------------------------------------------- top-k
+def test_topk_vs_selection_brute_force_with_ties():
+    g = synth.gen(9)
+    x = torch.round(torch.randn(3, 300, generator=g) * 4) / 4  # many exact ties
+    valid = [300, 150, 10]
+    want = brute.topk_fp64(x.numpy(), valid, 32)
+    got = ref.topk_rows(x, valid, 32)
+    assert np.array_equal(got.numpy().astype(np.int64), want)
+    assert torch.all(got[2, 10:] == -1)
