@@ -74,13 +74,16 @@ int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s
                 int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                 void* stream);
 
-/* Repack a canonical fp8 weight [N, K] (N % 16 == 0, K % 128 == 0) into MFMA operand
- * fragments for tl_fp8_gemm_packed: fragment (t, kb) (16 rows x 128 columns) occupies
- * 2048 contiguous bytes at (t * K/128 + kb) * 2048; within it, byte p*1024 + l*16 + i
- * (piece p in {0,1}, lane l in [0,64), i in [0,16)) is W[16 t + (l % 16)][128 kb +
- * 64 p + 16 (l / 16) + i].  packed must hold N*K bytes and not alias b.  Counterpart of
- * the reference's per-op weight converters (e.g. RMSNormProjQKVAFP8MMAWeightsConverter,
- * rmsnorm_projx_wqkva.py:18-119): a one-time, load-time layout change. */
+/* Repack a canonical fp8 weight [N, K] (N % 16 == 0, K % 512 == 0) into MFMA operand
+ * fragments for tl_fp8_gemm_packed.  Fragment (t, kb) -- rows 16t..16t+15, columns
+ * 128kb..128kb+127 -- is 2048 contiguous bytes at fragment index
+ * ((kb / 4) * (N/16) + t) * 4 + kb % 4 ("K-group-major": a workgroup's 4 K blocks per step
+ * are 8 KB of consecutive memory and neighbouring row tiles are neighbours); within it,
+ * byte p*1024 + l*16 + i (piece p in {0,1}, lane l in [0,64), i in [0,16)) is
+ * W[16 t + (l % 16)][128 kb + 64 p + 16 (l / 16) + i].  packed must hold N*K bytes and not
+ * alias b.  Counterpart of the reference's per-op weight converters (e.g.
+ * RMSNormProjQKVAFP8MMAWeightsConverter, rmsnorm_projx_wqkva.py:18-119): a one-time,
+ * load-time layout change. */
 int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* stream);
 
 /* tl_fp8_gemm with b in the fragment-packed layout of tl_fp8_pack_weight (same scales,
@@ -90,9 +93,15 @@ int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, co
                        void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Tile-major fragment packing for the MoE kernels: the stacked per-expert weights
+ * [rows, K] (rows % 16 == 0, K % 128 == 0) become fragments (t, kb) at (t*K/128 + kb)*2048
+ * with the in-fragment order of tl_fp8_pack_weight.  Load-time layout change (the role of
+ * ExpertSelectUpGateSiLUWeightsConverter / the down converters in the reference). */
+int tl_moe_pack_weight(const void* b, void* packed, int64_t rows, int64_t K, void* stream);
+
 /* MoE gate/up + SwiGLU at one expert-parallel shard (bf16 activations x fp8 weights,
  * the reference MoE's BF16MMA numerics).
- * x bf16 [M, D]; w13_packed = tl_fp8_pack_weight of the stacked per-expert gate/up
+ * x bf16 [M, D]; w13_packed = tl_moe_pack_weight of the stacked per-expert gate/up
  * weights [n_local * 2I, D] (expert e: rows e*2I .. e*2I+I-1 gate, then I rows up);
  * s13 fp32 [n_local, 2I/128, D/128].  topk_idx int32 [M, topk] holds global expert ids;
  * the shard owns ids [expert_begin, expert_begin + n_local).  Every local expert hit by
@@ -111,7 +120,7 @@ int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed, const floa
 
 /* MoE down projection + routing-weighted combine at one shard.
  * h bf16 [n_local, M, I] from tl_moe_gate_up_swiglu (same topk_idx); w2_packed =
- * tl_fp8_pack_weight of the stacked down weights [n_local * D, I]; s2 fp32
+ * tl_moe_pack_weight of the stacked down weights [n_local * D, I]; s2 fp32
  * [n_local, D/128, I/128]; topk_w fp32 [M, topk].
  *   y[t] = bf16( sum over the token's local experts e, ascending, of
  *                bf16(w[t,e] * (h[t,e] . D_e^T)) )   (fp32 sum)

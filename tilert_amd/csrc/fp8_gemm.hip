@@ -46,7 +46,23 @@ __device__ inline uint2 pack_bf16x4(v4f v) {
                     f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16));
 }
 
+// Fragment-packed layout ("K-group-major"): fragment (t, kb) -- 16 rows x 128 columns,
+// 2048 bytes in MFMA lane order -- lives at fragment index
+//   ((kb / 4) * NT + t) * 4 + kb % 4,      NT = N / 16,
+// so the 4 K blocks a 4-wave workgroup reads in one step are 8 KB of consecutive memory
+// and neighbouring row tiles' steps are neighbours: the whole grid sweeps the weight as
+// one moving window, the access pattern this memory system streams best.
+constexpr int kGroup = 4;
+
+__device__ inline size_t packed_fragment(int t, int kb, int NT) {
+  return ((static_cast<size_t>(kb / kGroup) * NT + t) * kGroup + (kb % kGroup)) * 2048;
+}
+
 // MT: 16-token tiles (M <= 16*MT); WAVES: waves per workgroup; PACKED: weight layout.
+// Every operand of the next K block -- weight fragment, activation block, both scales --
+// is requested one iteration ahead, so L2 latency of the activations hides behind the
+// current MFMA (measured: ~10% of the weight stream at M = 4).  Staging activations in
+// LDS instead was measured slower: its prologue costs what it saves.
 template <int MT, int WAVES, bool PACKED>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
@@ -54,6 +70,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
   __shared__ float red[WAVES - 1][MT][4][64];
   const int KB = K >> 7;
+  const int NT = N >> 4;
   const int ksplit = gridDim.y;
   const int ks = blockIdx.y;
   const int kb_begin = ks * kb_per_split;
@@ -63,26 +80,48 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
 
-  const uint8_t* brow = PACKED ? B + static_cast<size_t>(rt) * KB * 2048
-                               : B + static_cast<size_t>(n0 + r) * K;
+  const uint8_t* brow = B + static_cast<size_t>(n0 + r) * K;  // canonical layout
   const float* bs_row = Bs + static_cast<size_t>(n0 >> 7) * KB;
+  auto load_w = [&](int kb) -> v8i {
+    return PACKED ? load_packed_fragment(B + packed_fragment(rt, kb, NT), lane)
+                  : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
+  };
+  const bool tok0 = r < M;
+  auto load_x = [&](int kb) -> v8i {
+    return tok0 ? load_kblock(A + static_cast<size_t>(r) * K + kb * kBlock, g) : zero_v8i();
+  };
+  auto load_xs = [&](int kb) -> float { return tok0 ? As[static_cast<size_t>(r) * KB + kb] : 0.f; };
 
   v4f acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  for (int kb = kb_begin + wave; kb < kb_end; kb += WAVES) {
-    const v8i a = PACKED ? load_packed_fragment(brow + static_cast<size_t>(kb) * 2048, lane)
-                         : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
-    const float bsc = bs_row[kb];
+  int kb = kb_begin + wave;
+  v8i a_next = zero_v8i(), x_next = zero_v8i();
+  float xs_next = 0.f, bs_next = 0.f;
+  if (kb < kb_end) {
+    a_next = load_w(kb);
+    x_next = load_x(kb);
+    xs_next = load_xs(kb);
+    bs_next = bs_row[kb];
+  }
+  for (; kb < kb_end; kb += WAVES) {
+    const v8i a = a_next, x0 = x_next;
+    const float xs0 = xs_next, bsc = bs_next;
+    if (kb + WAVES < kb_end) {
+      a_next = load_w(kb + WAVES);
+      x_next = load_x(kb + WAVES);
+      xs_next = load_xs(kb + WAVES);
+      bs_next = bs_row[kb + WAVES];
+    }
+    acc[0] += mfma_16x16x128_fp8(a, x0) * (bsc * xs0);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 1; mt < MT; ++mt) {
       const int t = mt * 16 + r;
       const bool tok = t < M;
       const v8i x = tok ? load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g) : zero_v8i();
       const float xs = tok ? As[static_cast<size_t>(t) * KB + kb] : 0.f;
-      const v4f c = mfma_16x16x128_fp8(a, x);
-      acc[mt] += c * (bsc * xs);
+      acc[mt] += mfma_16x16x128_fp8(a, x) * (bsc * xs);
     }
   }
 
@@ -156,20 +195,38 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   if (lane == 0) __hip_atomic_store(&counters[rt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Pack a canonical [N, K] fp8 weight into MFMA fragments: fragment (rt, kb) is 2048
-// bytes at ((rt * KB) + kb) * 2048; piece p, lane l = r + 16 g holds the 16 bytes of row
-// rt*16 + r, columns kb*128 + 64 p + 16 g ... +15 at offset p*1024 + l*16.
+// Pack a canonical [N, K] fp8 weight into K-group-major MFMA fragments (see
+// packed_fragment): within fragment (t, kb), piece p, lane l = r + 16 g holds the 16
+// bytes of row 16 t + r, columns 128 kb + 64 p + 16 g ... +15, at offset p*1024 + l*16.
 __global__ __launch_bounds__(256) void pack_weight_kernel(const uint8_t* __restrict__ W,
                                                           uint8_t* __restrict__ P, int N, int K) {
   const int KB = K >> 7;
+  const int NT = N >> 4;
   const int64_t chunk = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;  // 16-byte chunk id
   const int64_t total = static_cast<int64_t>(N) * K / 16;
   if (chunk >= total) return;
-  const int64_t frag = chunk >> 7;  // 128 chunks per fragment
+  const int64_t frag = chunk >> 7;  // 128 chunks per fragment, tile-major source order
   const int within = static_cast<int>(chunk & 127);
   const int p = within >> 6, l = within & 63;
-  const int rt = static_cast<int>(frag / KB), kb = static_cast<int>(frag % KB);
-  const int row = rt * 16 + (l & 15);
+  const int t = static_cast<int>(frag / KB), kb = static_cast<int>(frag % KB);
+  const int row = t * 16 + (l & 15);
+  const int col = kb * 128 + 64 * p + 16 * (l >> 4);
+  *reinterpret_cast<uint4*>(P + packed_fragment(t, kb, NT) + within * 16) =
+      *reinterpret_cast<const uint4*>(W + static_cast<size_t>(row) * K + col);
+}
+
+// Tile-major fragment packing used by the MoE kernels: fragment (t, kb) at
+// (t * KB + kb) * 2048, same in-fragment order as above.
+__global__ __launch_bounds__(256) void pack_tile_major_kernel(const uint8_t* __restrict__ W,
+                                                              uint8_t* __restrict__ P, int N, int K) {
+  const int KB = K >> 7;
+  const int64_t chunk = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (chunk >= static_cast<int64_t>(N) * K / 16) return;
+  const int64_t frag = chunk >> 7;
+  const int within = static_cast<int>(chunk & 127);
+  const int p = within >> 6, l = within & 63;
+  const int t = static_cast<int>(frag / KB), kb = static_cast<int>(frag % KB);
+  const int row = t * 16 + (l & 15);
   const int col = kb * 128 + 64 * p + 16 * (l >> 4);
   reinterpret_cast<uint4*>(P)[chunk] = *reinterpret_cast<const uint4*>(W + static_cast<size_t>(row) * K + col);
 }
@@ -185,25 +242,26 @@ struct GemmPlan {
 // measured on MI355X, the split's extra round trips (partial store, counter, reload)
 // cost more than the better CU balance buys.  Narrow layers take the smallest split
 // giving >= 1024 workgroups (4 per CU), preferring a grid that is a whole multiple of
-// the 256 CUs, never leaving a slice empty.  Waves per workgroup: 8 when every wave
-// gets several K blocks, else 4.
+// the 256 CUs, with slices of whole K groups, never leaving a slice empty.
 static GemmPlan plan_gemm(int64_t N, int64_t K) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
+  const int groups = static_cast<int>(cdiv(KB, kGroup));
   p.row_tiles = static_cast<int>(N / 16);
   int s = 1;
   if (p.row_tiles < 512) {
     int smin = static_cast<int>(cdiv(1024, p.row_tiles));
-    if (smin > KB) smin = KB;
+    if (smin > groups) smin = groups;
     if (smin < 1) smin = 1;
     s = smin;
-    for (int c = smin; c <= 2 * smin && c <= KB; ++c) {
+    for (int c = smin; c <= 2 * smin && c <= groups; ++c) {
       if ((static_cast<int64_t>(p.row_tiles) * c) % 256 == 0) { s = c; break; }
     }
   }
-  p.kb_per_split = static_cast<int>(cdiv(KB, s));
+  p.kb_per_split = static_cast<int>(cdiv(groups, s)) * kGroup;
   p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
-  p.waves = p.kb_per_split >= 16 ? 8 : 4;
+  // wide layers: 8 waves (two K groups per step); split slices: 4 (one group)
+  p.waves = (p.ksplit == 1 && KB >= 32) ? 8 : kGroup;
   return p;
 }
 
@@ -280,7 +338,7 @@ extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const
 }
 
 extern "C" int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* stream) {
-  if (N <= 0 || K <= 0 || N % 16 || K % kBlock) { set_error("pack_weight: need N %% 16 == 0 and K %% 128 == 0 (N=%lld K=%lld)", (long long)N, (long long)K); return kErrArg; }
+  if (N <= 0 || K <= 0 || N % 16 || K % (kBlock * kGroup)) { set_error("pack_weight: need N %% 16 == 0 and K %% 512 == 0 (N=%lld K=%lld)", (long long)N, (long long)K); return kErrArg; }
   if (!b || !packed) { set_error("pack_weight: null pointer"); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(packed)) & 15) { set_error("pack_weight: pointers must be 16-byte aligned"); return kErrArg; }
   if (b == packed) { set_error("pack_weight: in-place packing is not supported"); return kErrArg; }
@@ -290,9 +348,20 @@ extern "C" int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_
   return check_launch("pack_weight");
 }
 
+extern "C" int tl_moe_pack_weight(const void* b, void* packed, int64_t rows, int64_t K, void* stream) {
+  if (rows <= 0 || K <= 0 || rows % 16 || K % kBlock) { set_error("moe_pack_weight: need rows %% 16 == 0 and K %% 128 == 0 (rows=%lld K=%lld)", (long long)rows, (long long)K); return kErrArg; }
+  if (!b || !packed) { set_error("moe_pack_weight: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(packed)) & 15) { set_error("moe_pack_weight: pointers must be 16-byte aligned"); return kErrArg; }
+  if (b == packed) { set_error("moe_pack_weight: in-place packing is not supported"); return kErrArg; }
+  hipLaunchKernelGGL(pack_tile_major_kernel, dim3(cdiv(rows * K / 16, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)b, (uint8_t*)packed, (int)rows, (int)K);
+  return check_launch("moe_pack_weight");
+}
+
 extern "C" int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed,
                                   const float* b_s, void* c_bf16, int64_t M, int64_t N, int64_t K,
                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (K % (kBlock * kGroup)) { set_error("fp8_gemm_packed: K=%lld must be a multiple of 512", (long long)K); return kErrArg; }
   const size_t need = tl_fp8_gemm_workspace_bytes(M, N, K);
   int rc = validate("fp8_gemm_packed", a, a_s, b_packed, b_s, c_bf16, M, N, K, workspace, workspace_bytes, need);
   if (rc) return rc;

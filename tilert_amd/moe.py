@@ -15,9 +15,16 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .kernel import _require_cuda, _stream, pack_weight
+from .kernel import _require_cuda, _stream
 
 BLOCK = 128
+
+
+def _pack(w: torch.Tensor) -> torch.Tensor:
+    rows, K = w.shape
+    out = torch.empty(rows * K, dtype=torch.uint8, device=w.device)
+    _lib.call("tl_moe_pack_weight", w.data_ptr(), out.data_ptr(), rows, K, _stream(w))
+    return out
 
 
 class LocalExperts:
@@ -40,8 +47,8 @@ class LocalExperts:
         self.n_local, self.I, self.D, self.expert_begin = E, I, D, expert_begin
         w13 = torch.cat([gate, up], dim=1).reshape(E * 2 * I, D).contiguous()
         self.s13 = torch.cat([gate_s, up_s], dim=1).float().contiguous()
-        self.w13 = pack_weight(w13, torch.empty(0, device=gate.device)).data
-        self.w2 = pack_weight(down.reshape(E * D, I).contiguous(), torch.empty(0, device=gate.device)).data
+        self.w13 = _pack(w13)
+        self.w2 = _pack(down.reshape(E * D, I).contiguous())
         self.s2 = down_s.float().contiguous()
 
     @property
