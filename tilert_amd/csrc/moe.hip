@@ -28,7 +28,9 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kMoeWaves = 4;
+constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups per CU)
+constexpr int kDownWaves = 16;      // down waves per workgroup: a tile's fragments spread wide
+constexpr int kDownSlots = 4;  // hit experts reduced together by the down kernel
 constexpr int kMaxLocalExperts = 64;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -84,19 +86,23 @@ __device__ inline v4f mfma_block_bf16(const v8i& w, float scale, const ActOperan
   return acc;
 }
 
-// Hit-expert bitmask of this shard, computed by the whole workgroup.
-__device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, int pairs, int e0,
-                                        int n_local, uint32_t* s_words) {
-  if (threadIdx.x < 2) s_words[threadIdx.x] = 0u;
-  __syncthreads();
-  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+// Hit-expert bitmask of this shard, computed by each wave on its own (no LDS, no
+// barrier): lanes test the routed ids, one ballot per local expert... folded as a
+// 64-bit OR across the wave's lanes with cross-lane exchanges.
+__device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, int pairs, int e0, int n_local) {
+  const int lane = threadIdx.x & 63;
+  uint64_t m = 0;
+  for (int i = lane; i < pairs; i += 64) {
     const int e = topk_idx[i] - e0;
-    if (e >= 0 && e < n_local) atomicOr(&s_words[e >> 5], 1u << (e & 31));
+    if (e >= 0 && e < n_local) m |= 1ull << e;
   }
-  __syncthreads();
-  const uint64_t m = static_cast<uint64_t>(s_words[0]) | (static_cast<uint64_t>(s_words[1]) << 32);
-  __syncthreads();
-  return m;
+  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo |= __shfl_xor(lo, o);
+    hi |= __shfl_xor(hi, o);
+  }
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
 }
 
 __device__ inline int nth_set_bit(uint64_t m, int n) {
@@ -108,13 +114,14 @@ __device__ inline float silu(float g) { return g / (1.0f + __expf(-g)); }
 
 // ---------------------------------------------------------------------- gate/up
 // Work item = (slot, 16-channel tile); a persistent grid strides over n_hit * I/16 items.
-__global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(
+// <= 128 VGPRs (4 waves per SIMD): two 8-wave workgroups per CU, so a 4-expert call's
+// 512 work items run in one generation
+__global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ topk_idx, int M, int topk, int e0, int n_local, int D, int I,
     uint16_t* __restrict__ h) {
-  __shared__ uint32_t s_words[2];
   __shared__ float red[kMoeWaves - 1][2][4][64];
-  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local, s_words);
+  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local);
   const int n_hit = __builtin_popcountll(mask);
   const int KB = D >> 7;
   const int tiles = I >> 4;
@@ -131,13 +138,36 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(
     const uint8_t* up = gate + static_cast<size_t>(tiles) * KB * 2048;
     const float* gs = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((rt * 16) >> 7)) * KB;
     const float* us = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((I + rt * 16) >> 7)) * KB;
+    // Every operand of the next K block (both fragments, the activation block, both
+    // scales) is requested one iteration ahead.  Vector loads retire in issue order, so a
+    // current-iteration load issued after a prefetch would make the wait cover the
+    // prefetch too; here the loop body only consumes registers loaded earlier.
     v4f ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = wave; kb < KB; kb += kMoeWaves) {
-      const v8i wg = load_fragment(gate + static_cast<size_t>(kb) * 2048, lane);
-      const v8i wu = load_fragment(up + static_cast<size_t>(kb) * 2048, lane);
-      const ActOperand xa = load_act(xrow + kb * kBlock, g, tok);
-      ag = mfma_block_bf16(wg, gs[kb], xa, ag);
-      au = mfma_block_bf16(wu, us[kb], xa, au);
+    int kb = wave;
+    v8i wg_n = zero_v8i(), wu_n = zero_v8i();
+    ActOperand xa_n = {};
+    float gs_n = 0.f, us_n = 0.f;
+    if (kb < KB) {
+      wg_n = load_fragment(gate + static_cast<size_t>(kb) * 2048, lane);
+      wu_n = load_fragment(up + static_cast<size_t>(kb) * 2048, lane);
+      xa_n = load_act(xrow + kb * kBlock, g, tok);
+      gs_n = gs[kb];
+      us_n = us[kb];
+    }
+    for (; kb < KB; kb += kMoeWaves) {
+      const v8i wg = wg_n, wu = wu_n;
+      const ActOperand xa = xa_n;
+      const float gsc = gs_n, usc = us_n;
+      const int kn = kb + kMoeWaves;
+      if (kn < KB) {
+        wg_n = load_fragment(gate + static_cast<size_t>(kn) * 2048, lane);
+        wu_n = load_fragment(up + static_cast<size_t>(kn) * 2048, lane);
+        xa_n = load_act(xrow + kn * kBlock, g, tok);
+        gs_n = gs[kn];
+        us_n = us[kn];
+      }
+      ag = mfma_block_bf16(wg, gsc, xa, ag);
+      au = mfma_block_bf16(wu, usc, xa, au);
     }
     if (wave > 0) {
 #pragma unroll
@@ -169,16 +199,18 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_gate_up_kernel(
 }
 
 // ---------------------------------------------------------------------- down + combine
-// One workgroup per 16-row output tile; slots are visited in ascending order and each
-// expert's term is reduced across waves, weighted, rounded to bf16 and accumulated in
-// fp32 -- a fixed order, so the result is deterministic.
-__global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(
+// One workgroup per 16-row output tile.  Hit experts are taken kDownSlots at a time; the
+// (slot, K block) items of a batch are dealt round-robin to the waves, each wave keeping
+// one fp32 accumulator per slot, so every wave has a weight fragment in flight for the
+// whole batch.  The per-slot partials are then reduced across waves in wave order and
+// wave 0 applies, slot by slot in ascending order, the routing weight and the per-term
+// bf16 rounding before the fp32 sum -- a fixed order, so the result is deterministic.
+__global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_kernel(
     const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int M, int topk, int e0,
     int n_local, int D, int I, uint16_t* __restrict__ y) {
-  __shared__ uint32_t s_words[2];
-  __shared__ float red[kMoeWaves - 1][4][64];
-  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local, s_words);
+  __shared__ float red[kDownWaves][kDownSlots][4][64];
+  const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local);
   const int n_hit = __builtin_popcountll(mask);
   const int KB = I >> 7;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -186,35 +218,88 @@ __global__ __launch_bounds__(kMoeWaves * 64) void moe_down_kernel(
   const bool tok = r < M;
   const int rt = blockIdx.x;
   v4f yacc = {0.f, 0.f, 0.f, 0.f};
+  // one routed (expert, weight) pair per lane, loaded now and consumed by the combine:
+  // no dependent loads after the weight stream (M * topk <= 64 here; larger is looped)
+  const int pairs = M * topk;
+  const int my_e = lane < pairs ? topk_idx[lane] - e0 : -1;
+  const float my_w = lane < pairs ? topk_w[lane] : 0.f;
 
-  for (int slot = 0; slot < n_hit; ++slot) {
-    const int e = nth_set_bit(mask, slot);
-    const uint8_t* wt = w2 + (static_cast<size_t>(e) * (D >> 4) + rt) * KB * 2048;
-    const float* sc = s2 + (static_cast<size_t>(e) * (D >> 7) + ((rt * 16) >> 7)) * KB;
-    const uint16_t* hrow = h + (static_cast<size_t>(slot) * M + (tok ? r : 0)) * I;
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    for (int kb = wave; kb < KB; kb += kMoeWaves) {
-      const v8i w = load_fragment(wt + static_cast<size_t>(kb) * 2048, lane);
-      const ActOperand xa = load_act(hrow + kb * kBlock, g, tok);
-      acc = mfma_block_bf16(w, sc[kb], xa, acc);
-    }
-    if (wave > 0) {
+  for (int s0 = 0; s0 < n_hit; s0 += kDownSlots) {
+    const int ns = min(kDownSlots, n_hit - s0);
+    int ex[kDownSlots];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave - 1][j][lane] = acc[j];
+    for (int j = 0; j < kDownSlots; ++j) ex[j] = j < ns ? nth_set_bit(mask, s0 + j) : 0;
+    v4f acc[kDownSlots];
+#pragma unroll
+    for (int j = 0; j < kDownSlots; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int items = ns * KB;  // item i = (slot i / KB, K block i % KB)
+    auto frag_of = [&](int it, int j) -> const uint8_t* {
+      return w2 + ((static_cast<size_t>(ex[j]) * (D >> 4) + rt) * KB + (it - j * KB)) * 2048;
+    };
+    // next item's fragment, activation block and scale are requested one iteration
+    // ahead (see the gate/up kernel for why all of them)
+    auto scale_of = [&](int it, int j) -> float {
+      return s2[(static_cast<size_t>(ex[j]) * (D >> 7) + ((rt * 16) >> 7)) * KB + (it - j * KB)];
+    };
+    auto act_of = [&](int it, int j) -> ActOperand {
+      const uint16_t* hrow = h + (static_cast<size_t>(s0 + j) * M + (tok ? r : 0)) * I;
+      return load_act(hrow + (it - j * KB) * kBlock, g, tok);
+    };
+    int it = wave;
+    v8i wn = zero_v8i();
+    ActOperand xn = {};
+    float sn = 0.f;
+    if (it < items) {
+      const int j = it / KB;
+      wn = load_fragment(frag_of(it, j), lane);
+      xn = act_of(it, j);
+      sn = scale_of(it, j);
     }
+    for (; it < items; it += kDownWaves) {
+      const int j = it / KB;
+      const v8i w = wn;
+      const ActOperand xa = xn;
+      const float sc = sn;
+      const int in = it + kDownWaves;
+      if (in < items) {
+        const int jn = in / KB;
+        wn = load_fragment(frag_of(in, jn), lane);
+        xn = act_of(in, jn);
+        sn = scale_of(in, jn);
+      }
+#pragma unroll
+      for (int jj = 0; jj < kDownSlots; ++jj)
+        if (jj == j) acc[jj] = mfma_block_bf16(w, sc, xa, acc[jj]);
+    }
+#pragma unroll
+    for (int j = 0; j < kDownSlots; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave][j][q][lane] = acc[j][q];
     __syncthreads();
     if (wave == 0) {
+      for (int j = 0; j < ns; ++j) {
+        v4f t = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kDownWaves; ++w)
 #pragma unroll
-      for (int w = 0; w < kMoeWaves - 1; ++w)
+          for (int q = 0; q < 4; ++q) t[q] += red[w][j][q][lane];
+        // routing weight of (token r, expert ex[j]); 0 when the token does not use it
+        float wj = 0.f;
+        for (int k = 0; k < topk; ++k) {
+          const int src = r * topk + k;
+          int e;
+          float v;
+          if (pairs <= 64) {
+            e = __shfl(my_e, src & 63);
+            v = __shfl(my_w, src & 63);
+          } else {
+            e = tok ? topk_idx[src] - e0 : -1;
+            v = tok ? topk_w[src] : 0.f;
+          }
+          if (tok && e == ex[j]) wj = v;
+        }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[j] += red[w][j][lane];
-      // routing weight of (token r, expert e); 0 when the token does not use it
-      float wr = 0.f;
-      if (tok)
-        for (int k = 0; k < topk; ++k)
-          if (topk_idx[r * topk + k] == e + e0) wr = topk_w[r * topk + k];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) yacc[j] += bf16_to_f32(f32_to_bf16(acc[j] * wr));
+        for (int q = 0; q < 4; ++q) yacc[q] += bf16_to_f32(f32_to_bf16(t[q] * wj));
+      }
     }
     __syncthreads();
   }
@@ -249,7 +334,7 @@ extern "C" int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed,
   if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed)) & 15) { set_error("moe_gate_up_swiglu: x and weights must be 16-byte aligned"); return kErrArg; }
   // enough workgroups for the largest possible hit set, capped at 4 per CU
   const int64_t max_items = n_local * (I / 16);
-  const int grid = static_cast<int>(max_items < 1024 ? max_items : 1024);
+  const int grid = static_cast<int>(max_items < 512 ? max_items : 512);  // 2 x 8 waves per CU
   hipLaunchKernelGGL(moe_gate_up_kernel, dim3(grid), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
                      (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx, (int)M, (int)topk,
                      (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
@@ -264,7 +349,7 @@ extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, co
   if (rc) return rc;
   if (!h_bf16 || !w2_packed || !s2 || !topk_idx || !topk_w || !y_bf16) { set_error("moe_down_combine: null pointer"); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15) { set_error("moe_down_combine: h and weights must be 16-byte aligned"); return kErrArg; }
-  hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kDownWaves * 64), 0, (hipStream_t)stream,
                      (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
                      (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)y_bf16);
   return check_launch("moe_down_combine");
