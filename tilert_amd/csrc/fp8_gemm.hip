@@ -60,9 +60,9 @@ __device__ inline size_t packed_fragment(int t, int kb, int NT) {
 
 // MT: 16-token tiles (M <= 16*MT); WAVES: waves per workgroup; PACKED: weight layout.
 // Every operand of the next K block -- weight fragment, activation block, both scales --
-// is requested one iteration ahead, so L2 latency of the activations hides behind the
-// current MFMA (measured: ~10% of the weight stream at M = 4).  Staging activations in
-// LDS instead was measured slower: its prologue costs what it saves.
+// is requested one block ahead, so L2 latency of the activations hides behind the
+// current MFMA.  Staging activations in LDS instead was measured slower: its prologue
+// costs what it saves.
 template <int MT, int WAVES, bool PACKED>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
@@ -86,42 +86,60 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     return PACKED ? load_packed_fragment(B + packed_fragment(rt, kb, NT), lane)
                   : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
   };
-  const bool tok0 = r < M;
-  auto load_x = [&](int kb) -> v8i {
-    return tok0 ? load_kblock(A + static_cast<size_t>(r) * K + kb * kBlock, g) : zero_v8i();
-  };
-  auto load_xs = [&](int kb) -> float { return tok0 ? As[static_cast<size_t>(r) * KB + kb] : 0.f; };
+  // Activation rows past M are read from row M-1 and zeroed afterwards, so every load
+  // in the loop below is unconditional: the compiler's wait-count pass can then wait for
+  // exactly the operands an MFMA needs instead of for everything in flight.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
 
   v4f acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  int kb = kb_begin + wave;
-  v8i a_next = zero_v8i(), x_next = zero_v8i();
-  float xs_next = 0.f, bs_next = 0.f;
-  if (kb < kb_end) {
-    a_next = load_w(kb);
-    x_next = load_x(kb);
-    xs_next = load_xs(kb);
-    bs_next = bs_row[kb];
-  }
-  for (; kb < kb_end; kb += WAVES) {
-    const v8i a = a_next, x0 = x_next;
-    const float xs0 = xs_next, bsc = bs_next;
-    if (kb + WAVES < kb_end) {
-      a_next = load_w(kb + WAVES);
-      x_next = load_x(kb + WAVES);
-      xs_next = load_xs(kb + WAVES);
-      bs_next = bs_row[kb + WAVES];
-    }
-    acc[0] += mfma_16x16x128_fp8(a, x0) * (bsc * xs0);
+  // Ping-pong over two operand buffers (the loop is unrolled by two) so the next K
+  // block's loads are in flight during this block's MFMAs.  A `cur = next` rotation
+  // would make the compiler copy registers at the end of each iteration -- and wait for
+  // the loads in flight to do so, serialising the stream.
+  struct Ops {
+    v8i a, x[MT];
+    float xs[MT], bs;
+  };
+  auto fetch = [&](int kb, Ops& o) {
+    o.a = load_w(kb);
 #pragma unroll
-    for (int mt = 1; mt < MT; ++mt) {
-      const int t = mt * 16 + r;
-      const bool tok = t < M;
-      const v8i x = tok ? load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g) : zero_v8i();
-      const float xs = tok ? As[static_cast<size_t>(t) * KB + kb] : 0.f;
-      acc[mt] += mfma_16x16x128_fp8(a, x) * (bsc * xs);
+    for (int mt = 0; mt < MT; ++mt) {
+      const int t = min(mt * 16 + r, M - 1);
+      o.x[mt] = load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g);
+      o.xs[mt] = As[static_cast<size_t>(t) * KB + kb];
+    }
+    o.bs = bs_row[kb];
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads issued ahead of the MFMAs after them
+  };
+  auto compute = [&](const Ops& o) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float xs = mt * 16 + r < M ? o.xs[mt] : 0.f;  // zero rows past M
+      acc[mt] += mfma_16x16x128_fp8(o.a, o.x[mt]) * (o.bs * xs);
+    }
+  };
+  // this wave's K blocks: kb_begin + wv + i*WAVES, i < n
+  const int kb0 = kb_begin + wv;
+  const int n = kb0 < kb_end ? (kb_end - kb0 + WAVES - 1) / WAVES : 0;
+  Ops b0, b1;
+  if (n > 0) {
+    fetch(kb0, b0);
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      fetch(kb0 + (i + 1) * WAVES, b1);
+      compute(b0);
+      fetch(kb0 + (i + 2) * WAVES, b0);
+      compute(b1);
+    }
+    if (i + 1 < n) {
+      fetch(kb0 + (i + 1) * WAVES, b1);
+      compute(b0);
+      compute(b1);
+    } else {
+      compute(b0);
     }
   }
 

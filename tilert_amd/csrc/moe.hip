@@ -29,7 +29,7 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups per CU)
-constexpr int kDownWaves = 16;      // down waves per workgroup: a tile's fragments spread wide
+constexpr int kDownWaves = 8;       // down waves per workgroup
 constexpr int kDownSlots = 4;  // hit experts reduced together by the down kernel
 constexpr int kMaxLocalExperts = 64;
 
@@ -245,31 +245,35 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_kernel(
       const uint16_t* hrow = h + (static_cast<size_t>(s0 + j) * M + (tok ? r : 0)) * I;
       return load_act(hrow + (it - j * KB) * kBlock, g, tok);
     };
-    int it = wave;
-    v8i wn = zero_v8i();
-    ActOperand xn = {};
-    float sn = 0.f;
-    if (it < items) {
-      const int j = it / KB;
-      wn = load_fragment(frag_of(it, j), lane);
-      xn = act_of(it, j);
-      sn = scale_of(it, j);
-    }
-    for (; it < items; it += kDownWaves) {
-      const int j = it / KB;
-      const v8i w = wn;
-      const ActOperand xa = xn;
-      const float sc = sn;
-      const int in = it + kDownWaves;
-      if (in < items) {
-        const int jn = in / KB;
-        wn = load_fragment(frag_of(in, jn), lane);
-        xn = act_of(in, jn);
-        sn = scale_of(in, jn);
-      }
+    // Ping-pong over two operand buffers (the loop is unrolled by two) so the next item's
+    // loads are in flight during this one's MFMAs. A plain `cur = next` rotation makes the
+    // compiler copy registers at the end of each iteration, waiting for those loads.
+    struct Ops {
+      v8i w;
+      ActOperand xa;
+      float sc;
+      int j;
+    };
+    auto fetch = [&](int it, Ops& o) {
+      o.j = it / KB;
+      o.w = load_fragment(frag_of(it, o.j), lane);
+      o.xa = act_of(it, o.j);
+      o.sc = scale_of(it, o.j);
+    };
+    auto compute = [&](const Ops& o) {
 #pragma unroll
       for (int jj = 0; jj < kDownSlots; ++jj)
-        if (jj == j) acc[jj] = mfma_block_bf16(w, sc, xa, acc[jj]);
+        if (jj == o.j) acc[jj] = mfma_block_bf16(o.w, o.sc, o.xa, acc[jj]);
+    };
+    constexpr int W = kDownWaves;
+    Ops b0, b1;
+    if (wave < items) fetch(wave, b0);
+    for (int it = wave; it < items; it += 2 * W) {
+      if (it + W < items) fetch(it + W, b1);
+      compute(b0);
+      if (it + W >= items) break;
+      if (it + 2 * W < items) fetch(it + 2 * W, b0);
+      compute(b1);
     }
 #pragma unroll
     for (int j = 0; j < kDownSlots; ++j)
