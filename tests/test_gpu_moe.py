@@ -44,6 +44,8 @@ def _run(M, E, D, I, topk, n_experts, e0, seed, idx=None, w=None):
     (1, 4, 1024, 512, 8, 16, 4),
     (16, 8, 256, 384, 4, 16, 8),
     (3, 32, 7168, 2048, 8, 256, 32),  # config 2 shapes (shard 1 of 8)
+    (16, 8, 512, 256, 8, 32, 0),  # 128 routed pairs: the kernels without LDS activations
+    (8, 4, 7168, 256, 2, 16, 0),  # x [8, 7168] exceeds 64 KB: gate/up without LDS, down with
 ])
 def test_moe_vs_oracle(cuda, M, E, D, I, topk, n_exp, e0):
     y, ry, hits = _run(M, E, D, I, topk, n_exp, e0, seed=M * 1000 + E + D)

@@ -4,6 +4,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
@@ -24,6 +28,26 @@ int check_launch(const char* what) {
     set_error("%s: launch failed: %s", what, hipGetErrorString(e));
     return kErrHip;
   }
+  return kOk;
+}
+
+int allow_dynamic_lds(const void* kernel, int bytes, const char* who) {
+  static std::mutex mu;
+  static std::set<std::pair<int, const void*>> done;  // (device, kernel) already raised
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("%s: hipGetDevice failed: %s", who, hipGetErrorString(e));
+    return kErrHip;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({dev, kernel})) return kOk;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) {
+    set_error("%s: hipFuncSetAttribute failed: %s", who, hipGetErrorString(e));
+    return kErrHip;
+  }
+  done.insert({dev, kernel});
   return kOk;
 }
 

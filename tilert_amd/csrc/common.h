@@ -22,6 +22,9 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 // ---------------------------------------------------------------- error reporting
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+// Raise a kernel's dynamic-LDS limit to `bytes` (gfx950 has 160 KB per CU; launches
+// above 64 KB need it), once per (device, kernel); thread-safe.
+int allow_dynamic_lds(const void* kernel, int bytes, const char* who);
 
 enum Status { kOk = 0, kErrArg = 1, kErrHip = 2, kErrUnsupported = 3 };
 
@@ -99,6 +102,61 @@ __device__ inline v8i zero_v8i() {
 #pragma unroll
   for (int i = 0; i < 8; ++i) r[i] = 0;
   return r;
+}
+
+// A wave-uniform float read through the vector memory path.  Scalar loads share their
+// wait counter with LDS reads, and SMEM returns out of order, so every wait on an LDS
+// read would also wait for a scalar prefetch; a vector load is counted in issue order
+// with the other prefetched operands instead.
+__device__ inline float load_f32_vector(const float* p) {
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));  // hides the uniform address
+  return p[zero];
+}
+
+// Software pipeline over n items with D operand buffers: item i's loads are issued D-1
+// items ahead of its compute.  fetch(i, buf) must issue the same, unconditional loads for
+// every i, so the steady-state loop has a fixed number of loads in flight and the
+// compiler's wait counts cover only the operands being consumed.  Buffer indices are
+// compile-time constants (the loop is unrolled by D), so no register copies -- which
+// would wait for the loads -- are needed.  The last 2D-2 items run in a guarded tail.
+// start() runs once, after the first fetches are issued and before the first compute
+// (for work that should overlap them, e.g. filling LDS); it runs even when n == 0, so it
+// may contain a workgroup barrier as long as every wave calls ring_pipeline.
+template <int D, class Buf, class Fetch, class Compute, class Start>
+__device__ inline void ring_pipeline(int n, Buf (&buf)[D], Fetch&& fetch, Compute&& compute, Start&& start) {
+  if (n < D - 1) {  // too short to fill the ring
+    if (n > 0) fetch(0, buf[0]);
+    start();
+    for (int i = 0; i < n; ++i) {
+      if (i > 0) fetch(i, buf[0]);
+      compute(i, buf[0]);
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j) fetch(j, buf[j]);
+  start();
+  int i = 0;
+  for (; i + 2 * D - 2 < n; i += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      fetch(i + j + D - 1, buf[(j + D - 1) % D]);
+      compute(i + j, buf[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 2 * D - 2; ++j) {
+    if (i + j < n) {
+      if (i + j + D - 1 < n) fetch(i + j + D - 1, buf[(j + D - 1) % D]);
+      compute(i + j, buf[j % D]);
+    }
+  }
+}
+
+template <int D, class Buf, class Fetch, class Compute>
+__device__ inline void ring_pipeline(int n, Buf (&buf)[D], Fetch&& fetch, Compute&& compute) {
+  ring_pipeline(n, buf, fetch, compute, [] {});
 }
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

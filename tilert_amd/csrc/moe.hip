@@ -19,6 +19,8 @@
 // Weight layout: the fragment-packed layout of tl_fp8_pack_weight applied to the stacked
 // per-expert matrices: gate/up as w13 [E][2I rows (gate then up)][D], down as
 // w2 [E][D rows][I]; scales [E][2I/128][D/128] and [E][D/128][I/128].
+#include <algorithm>
+
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
@@ -102,6 +104,10 @@ __device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, in
     lo |= __shfl_xor(lo, o);
     hi |= __shfl_xor(hi, o);
   }
+  // every lane now holds the same mask: make that visible to the compiler, so the hit
+  // count, expert ids and weight addresses derived from it live in scalar registers
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
   return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
 }
 
@@ -111,6 +117,275 @@ __device__ inline int nth_set_bit(uint64_t m, int n) {
 }
 
 __device__ inline float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// One routed (expert, weight) pair per lane, loaded at kernel start and read back with
+// lane shuffles by routing_weight: no dependent loads after the weight stream.
+// The loads are unconditional (lanes past `pairs` reread the last pair), so wait counts
+// for loads issued after them stay exact.
+__device__ inline int lane_pair_expert(const int32_t* __restrict__ topk_idx, int pairs, int e0) {
+  const int lane = threadIdx.x & 63;
+  const int v = topk_idx[min(lane, pairs - 1)];
+  return lane < pairs ? v - e0 : -1;
+}
+__device__ inline float lane_pair_weight(const float* __restrict__ topk_w, int pairs) {
+  const int lane = threadIdx.x & 63;
+  const float v = topk_w[min(lane, pairs - 1)];
+  return lane < pairs ? v : 0.f;
+}
+
+// Hit-expert bitmask from the lane-held pairs (pairs <= 64), wave-uniform.
+__device__ inline uint64_t lane_pairs_mask(int my_e, int n_local) {
+  const uint64_t m = (my_e >= 0 && my_e < n_local) ? (1ull << my_e) : 0ull;
+  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo |= __shfl_xor(lo, o);
+    hi |= __shfl_xor(hi, o);
+  }
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
+// Routing weight of (token r, local expert e); 0 when the token does not use it.  Pairs
+// beyond the 64 held by the lanes are read from memory.
+__device__ inline float routing_weight(const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w,
+                                       int my_e, float my_w, int pairs, int topk, int e0, int r, bool tok, int e) {
+  float wj = 0.f;
+  for (int k = 0; k < topk; ++k) {
+    const int src = r * topk + k;
+    int ee;
+    float v;
+    if (pairs <= 64) {
+      ee = __shfl(my_e, src & 63);
+      v = __shfl(my_w, src & 63);
+    } else {
+      ee = tok ? topk_idx[src] - e0 : -1;
+      v = tok ? topk_w[src] : 0.f;
+    }
+    if (tok && ee == e) wj = v;
+  }
+  return wj;
+}
+
+// The activation operand read from LDS: lane (r, g) takes row `row` (token r, clamped
+// to a valid row: columns past M are never stored) at the lane group's K offsets.
+__device__ inline ActOperand lds_act(const uint16_t* row_kblock, int g) {
+  ActOperand o;
+  const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.v[j] = *reinterpret_cast<const v8bf*>(row_kblock + off[j]);
+  return o;
+}
+
+// Workgroup-wide copy of n16 16-byte chunks (n16 <= kStageChunks * blockDim.x) from global
+// memory into LDS, split in two so other loads can be issued in between: stage_issue
+// issues a FIXED number of loads per thread (surplus threads reload the last chunk), so
+// the compiler's wait counts for the loads issued before it stay exact; stage_commit
+// writes the chunks to LDS once they have arrived.
+constexpr int kStageChunks = 8;  // 64 KB with 512 threads
+struct Staged {
+  u32x4 v[kStageChunks];
+};
+__device__ inline Staged stage_issue(const void* src, int n16) {
+  const u32x4* s = reinterpret_cast<const u32x4*>(src);
+  Staged st;
+#pragma unroll
+  for (int u = 0; u < kStageChunks; ++u) st.v[u] = s[min(static_cast<int>(threadIdx.x + u * blockDim.x), n16 - 1)];
+  return st;
+}
+__device__ inline void stage_commit(void* lds, const Staged& st, int n16) {
+  u32x4* d = reinterpret_cast<u32x4*>(lds);
+#pragma unroll
+  for (int u = 0; u < kStageChunks; ++u) {
+    const int c = threadIdx.x + u * blockDim.x;
+    if (c < n16) d[c] = st.v[u];
+  }
+}
+
+constexpr int kGuDepth = 2;  // weight blocks in flight per wave (gate/up, LDS activations)
+constexpr int kDnDepth = 4;  // down items in flight per wave (LDS activations)
+constexpr int kLdsActBytes = 64 * 1024;  // activation staging limit (2 workgroups per CU)
+
+// ------------------------------------------------------ gate/up, LDS activations
+// Used when x [M, D] bf16 fits in 64 KB (M <= 4 at D = 7168).  The workgroup stages x in
+// LDS once; the waves then stream only weight fragments, kGuDepth blocks ahead through
+// ring_pipeline, and read their activation operands from LDS, so nothing but the weight
+// stream is waited on.  Work items, reduction and output as in moe_gate_up_kernel.
+__global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13, const float* __restrict__ s13,
+    const int32_t* __restrict__ topk_idx, int M, int topk, int e0, int n_local, int D, int I,
+    uint16_t* __restrict__ h) {
+  extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
+  __shared__ float red[kMoeWaves - 1][2][4][64];
+  // the routing and the x staging loads are in flight together (one round trip)
+  const int pairs = M * topk;
+  const int lane = threadIdx.x & 63;
+  const int raw_e = topk_idx[min(lane, pairs - 1)];
+  const int x16 = M * D / 8;
+  stage_commit(xl, stage_issue(x, x16), x16);
+  const uint64_t mask = lane_pairs_mask(lane < pairs ? raw_e - e0 : -1, n_local);
+  const int n_hit = __builtin_popcountll(mask);
+  const int KB = D >> 7;
+  const int tiles = I >> 4;
+  const int rows_e = 2 * I;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int r = lane & 15, g = lane >> 4;
+  const uint16_t* xrow = xl + min(r, M - 1) * D;
+  const int n = wave < KB ? (KB - wave + kMoeWaves - 1) / kMoeWaves : 0;  // K blocks wave + i*8
+  __syncthreads();
+
+  for (int item = blockIdx.x; item < n_hit * tiles; item += gridDim.x) {
+    const int slot = item / tiles, rt = item - slot * tiles;
+    const int e = nth_set_bit(mask, slot);
+    const uint8_t* gate = w13 + (static_cast<size_t>(e) * (rows_e >> 4) + rt) * KB * 2048;
+    const uint8_t* up = gate + static_cast<size_t>(tiles) * KB * 2048;
+    const float* gs = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((rt * 16) >> 7)) * KB;
+    const float* us = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((I + rt * 16) >> 7)) * KB;
+    v4f ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    struct Ops {
+      v8i wg, wu;
+      float gs, us;
+    };
+    Ops buf[kGuDepth];
+    ring_pipeline(
+        n, buf,
+        [&](int i, Ops& o) {
+          const int kb = wave + i * kMoeWaves;
+          o.wg = load_fragment(gate + static_cast<size_t>(kb) * 2048, lane);
+          o.wu = load_fragment(up + static_cast<size_t>(kb) * 2048, lane);
+          o.gs = load_f32_vector(gs + kb);
+          o.us = load_f32_vector(us + kb);
+        },
+        [&](int i, const Ops& o) {
+          const int kb = wave + i * kMoeWaves;
+          const uint16_t* xk = xrow + kb * kBlock;
+          const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {  // one 32-wide K step at a time: few live registers
+            const v8bf xa = *reinterpret_cast<const v8bf*>(xk + off[j]);
+            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wg[2 * j], o.wg[2 * j + 1], o.gs), xa, ag, 0, 0, 0);
+            au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wu[2 * j], o.wu[2 * j + 1], o.us), xa, au, 0, 0, 0);
+          }
+        });
+    if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[wave - 1][0][j][lane] = ag[j];
+        red[wave - 1][1][j][lane] = au[j];
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < kMoeWaves - 1; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ag[j] += red[w][0][j][lane];
+          au[j] += red[w][1][j][lane];
+        }
+      if (r < M) {
+        uint16_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16(silu(ag[j]) * au[j]);
+        uint16_t* dst = h + (static_cast<size_t>(slot) * M + r) * I + rt * 16 + 4 * g;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                    o[2] | (static_cast<uint32_t>(o[3]) << 16));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------ down, LDS activations
+// Used when one hit expert's h rows [M, I] fit in 64 KB.  Hit experts are taken
+// `sb` at a time (sb * M * I * 2 <= 64 KB); the batch's h rows are staged in LDS and the
+// (slot, K block) items dealt round-robin to the waves are streamed kDnDepth ahead through
+// ring_pipeline, one fp32 accumulator per slot.  After the stream the same LDS holds the
+// cross-wave partials; wave 0 combines exactly as moe_down_kernel does.
+__global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
+    const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int M, int topk, int e0,
+    int n_local, int D, int I, int sb, uint16_t* __restrict__ y) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint16_t* hl = reinterpret_cast<uint16_t*>(smem);  // [sb][M][I] during the stream
+  float(*red)[kDownSlots][4][64] = reinterpret_cast<float(*)[kDownSlots][4][64]>(smem);  // after it
+  const int pairs = M * topk;
+  const int my_e = lane_pair_expert(topk_idx, pairs, e0);
+  const float my_w = lane_pair_weight(topk_w, pairs);
+  const uint64_t mask = lane_pairs_mask(my_e, n_local);
+  const int n_hit = __builtin_popcountll(mask);
+  const int KB = I >> 7;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int r = lane & 15, g = lane >> 4;
+  const bool tok = r < M;
+  const int row = min(r, M - 1);
+  const int rt = blockIdx.x;
+  v4f yacc = {0.f, 0.f, 0.f, 0.f};
+
+  for (int s0 = 0; s0 < n_hit; s0 += sb) {
+    const int ns = min(sb, n_hit - s0);
+    const int h16 = ns * M * I / 8;
+    v4f acc[kDownSlots];
+#pragma unroll
+    for (int j = 0; j < kDownSlots; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int items = ns * KB;  // item = (slot it / KB, K block it % KB)
+    const int n = wave < items ? (items - wave + kDownWaves - 1) / kDownWaves : 0;
+    struct Ops {
+      v8i w;
+      float sc;
+    };
+    Ops buf[kDnDepth];
+    ring_pipeline(
+        n, buf,
+        [&](int i, Ops& o) {
+          const int it = wave + i * kDownWaves;
+          const int j = it / KB, kb = it - j * KB;
+          const int e = nth_set_bit(mask, s0 + j);  // scalar bit arithmetic (no indexed array)
+          const uint8_t* f = w2 + (static_cast<size_t>(e) * (D >> 4) + rt) * KB * 2048;
+          const float* sp = s2 + (static_cast<size_t>(e) * (D >> 7) + ((rt * 16) >> 7)) * KB;
+          o.w = load_fragment(f + static_cast<size_t>(kb) * 2048, lane);
+          o.sc = load_f32_vector(sp + kb);
+        },
+        [&](int i, const Ops& o) {
+          const int it = wave + i * kDownWaves;
+          const int j = it / KB, kb = it - j * KB;
+          const ActOperand xa = lds_act(hl + (j * M + row) * I + kb * kBlock, g);
+#pragma unroll
+          for (int jj = 0; jj < kDownSlots; ++jj)
+            if (jj == j) acc[jj] = mfma_block_bf16(o.w, o.sc, xa, acc[jj]);
+        },
+        [&] {  // the batch's h rows into LDS while the first weight fetches are in flight
+          stage_commit(hl, stage_issue(h + static_cast<size_t>(s0) * M * I, h16), h16);
+          __syncthreads();
+        });
+    __syncthreads();  // every wave is done with hl before it becomes the partials
+#pragma unroll
+    for (int j = 0; j < kDownSlots; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave][j][q][lane] = acc[j][q];
+    __syncthreads();
+    if (wave == 0) {
+      for (int j = 0; j < ns; ++j) {
+        v4f t = {0.f, 0.f, 0.f, 0.f};
+        for (int w = 0; w < kDownWaves; ++w)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) t[q] += red[w][j][q][lane];
+        const float wj = routing_weight(topk_idx, topk_w, my_e, my_w, pairs, topk, e0, r, tok, nth_set_bit(mask, s0 + j));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) yacc[q] += bf16_to_f32(f32_to_bf16(t[q] * wj));
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && tok) {
+    uint16_t* dst = y + static_cast<size_t>(r) * D + rt * 16 + 4 * g;
+    *reinterpret_cast<uint2*>(dst) =
+        make_uint2(f32_to_bf16(yacc[0]) | (static_cast<uint32_t>(f32_to_bf16(yacc[1])) << 16),
+                   f32_to_bf16(yacc[2]) | (static_cast<uint32_t>(f32_to_bf16(yacc[3])) << 16));
+  }
+}
 
 // ---------------------------------------------------------------------- gate/up
 // Work item = (slot, 16-channel tile); a persistent grid strides over n_hit * I/16 items.
@@ -221,8 +496,8 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_kernel(
   // one routed (expert, weight) pair per lane, loaded now and consumed by the combine:
   // no dependent loads after the weight stream (M * topk <= 64 here; larger is looped)
   const int pairs = M * topk;
-  const int my_e = lane < pairs ? topk_idx[lane] - e0 : -1;
-  const float my_w = lane < pairs ? topk_w[lane] : 0.f;
+  const int my_e = lane_pair_expert(topk_idx, pairs, e0);
+  const float my_w = lane_pair_weight(topk_w, pairs);
 
   for (int s0 = 0; s0 < n_hit; s0 += kDownSlots) {
     const int ns = min(kDownSlots, n_hit - s0);
@@ -286,21 +561,7 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_kernel(
         for (int w = 0; w < kDownWaves; ++w)
 #pragma unroll
           for (int q = 0; q < 4; ++q) t[q] += red[w][j][q][lane];
-        // routing weight of (token r, expert ex[j]); 0 when the token does not use it
-        float wj = 0.f;
-        for (int k = 0; k < topk; ++k) {
-          const int src = r * topk + k;
-          int e;
-          float v;
-          if (pairs <= 64) {
-            e = __shfl(my_e, src & 63);
-            v = __shfl(my_w, src & 63);
-          } else {
-            e = tok ? topk_idx[src] - e0 : -1;
-            v = tok ? topk_w[src] : 0.f;
-          }
-          if (tok && e == ex[j]) wj = v;
-        }
+        const float wj = routing_weight(topk_idx, topk_w, my_e, my_w, pairs, topk, e0, r, tok, ex[j]);
 #pragma unroll
         for (int q = 0; q < 4; ++q) yacc[q] += bf16_to_f32(f32_to_bf16(t[q] * wj));
       }
@@ -339,9 +600,18 @@ extern "C" int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed,
   // enough workgroups for the largest possible hit set, capped at 4 per CU
   const int64_t max_items = n_local * (I / 16);
   const int grid = static_cast<int>(max_items < 512 ? max_items : 512);  // 2 x 8 waves per CU
-  hipLaunchKernelGGL(moe_gate_up_kernel, dim3(grid), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
-                     (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx, (int)M, (int)topk,
-                     (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
+  const int64_t x_bytes = M * D * 2;
+  if (x_bytes <= kLdsActBytes && M * topk <= 64) {  // activations staged in LDS, routing in lanes
+    rc = allow_dynamic_lds(reinterpret_cast<const void*>(moe_gate_up_lds_kernel), kLdsActBytes, "moe_gate_up_swiglu");
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_gate_up_lds_kernel, dim3(grid), dim3(kMoeWaves * 64), static_cast<size_t>(x_bytes),
+                       (hipStream_t)stream, (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx,
+                       (int)M, (int)topk, (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
+  } else {
+    hipLaunchKernelGGL(moe_gate_up_kernel, dim3(grid), dim3(kMoeWaves * 64), 0, (hipStream_t)stream,
+                       (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx, (int)M, (int)topk,
+                       (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
+  }
   return check_launch("moe_gate_up_swiglu");
 }
 
@@ -353,8 +623,20 @@ extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, co
   if (rc) return rc;
   if (!h_bf16 || !w2_packed || !s2 || !topk_idx || !topk_w || !y_bf16) { set_error("moe_down_combine: null pointer"); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15) { set_error("moe_down_combine: h and weights must be 16-byte aligned"); return kErrArg; }
-  hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kDownWaves * 64), 0, (hipStream_t)stream,
-                     (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
-                     (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)y_bf16);
+  const int64_t h_bytes = M * I * 2;  // one hit expert's h rows
+  if (h_bytes <= kLdsActBytes && M * topk <= 64) {  // activations staged in LDS, sb hit experts per batch
+    const int sb = static_cast<int>(std::min<int64_t>(kDownSlots, kLdsActBytes / h_bytes));
+    const size_t red_bytes = sizeof(float) * kDownWaves * kDownSlots * 4 * 64;
+    const size_t lds = std::max<size_t>(static_cast<size_t>(sb) * h_bytes, red_bytes);
+    rc = allow_dynamic_lds(reinterpret_cast<const void*>(moe_down_lds_kernel), kLdsActBytes, "moe_down_combine");
+    if (rc) return rc;
+    hipLaunchKernelGGL(moe_down_lds_kernel, dim3(D / 16), dim3(kDownWaves * 64), lds, (hipStream_t)stream,
+                       (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
+                       (int)expert_begin, (int)n_local, (int)D, (int)I, sb, (uint16_t*)y_bf16);
+  } else {
+    hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kDownWaves * 64), 0, (hipStream_t)stream,
+                       (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
+                       (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)y_bf16);
+  }
   return check_launch("moe_down_combine");
 }

@@ -18,7 +18,6 @@
 // work on its stream; the wait is bounded (about a second) so a wave can never hang.
 //
 // Rows are the topk_accurate samples: row i considers columns [0, valid_base + 1 + i).
-#include <mutex>
 
 #include "common.h"
 #include "../../include/tilert_amd.h"
@@ -291,13 +290,8 @@ extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64
   if (!workspace || workspace_bytes < need) { set_error("topk: workspace of %zu bytes required (got %zu)", need, workspace_bytes); return kErrArg; }
   const TopkWs ws = carve(workspace, rows);
   const size_t lds = static_cast<size_t>(chunks) * kBins * sizeof(uint32_t);
-  static std::once_flag once;  // allow the >64 KB dynamic LDS gfx950 offers (160 KB per CU)
-  static hipError_t attr_rc = hipSuccess;
-  std::call_once(once, [] {
-    attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(topk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  kMaxChunks * kBins * static_cast<int>(sizeof(uint32_t)));
-  });
-  if (attr_rc != hipSuccess) { set_error("topk: hipFuncSetAttribute failed: %s", hipGetErrorString(attr_rc)); return kErrHip; }
+  const int rc = allow_dynamic_lds(reinterpret_cast<const void*>(topk_kernel), kMaxChunks * kBins * static_cast<int>(sizeof(uint32_t)), "topk");
+  if (rc) return rc;
   hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), dim3(kTkThreads),
                      lds, (hipStream_t)stream, logits, ld, valid_base, (int)k, ws, out);
   return check_launch("topk");
