@@ -5,98 +5,203 @@
 // fp8 cache layout of pd_vllm/profiles/mla_nsa.py:211-228).
 //
 // gfx950 mapping: the M*H query rows form M*H/16 tiles of 16 rows x 128 dims, staged
-// once per workgroup through LDS and held in registers for the whole kernel (A operand);
-// each wave streams its own range of 16-key tiles (B operand, 2 KB contiguous each, one
-// tile prefetched ahead) through the native fp8 MFMA v_mfma_f32_16x16x128_f8f6f4 -- one
+// once per workgroup through LDS (in MFMA fragment order); each wave holds the tiles of
+// its tokens in registers (A operand) and takes its own range of 16-key tiles (B operand,
+// 2 KB contiguous each) through the native fp8 MFMA v_mfma_f32_16x16x128_f8f6f4 -- one
 // MFMA is a whole 128-long dot product for 16 heads x 16 keys.  Epilogue per MFMA: ReLU
-// and the head weight (2 VALU ops per element, weights read from LDS); the head sum over
-// a lane's 4 heads and a token's tiles stays in registers, and the 4 lane groups are
-// combined with v_permlane32_swap / v_permlane16_swap.
+// (one integer max) and the head weight (one FMA); the head sum over a lane's 4 heads
+// and a token's tiles stays in registers, and the 4 lane groups are combined with
+// v_permlane32_swap / v_permlane16_swap.
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
 namespace tl {
 
-constexpr int kIdxWaves = 8;
+// ReLU as one integer max on the bit pattern (negative floats are negative integers):
+// fmaxf(x, 0) costs two instructions under IEEE mode (a NaN-quieting max first).
+__device__ inline float relu(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 
-template <int M, int H>
+constexpr int kIdxWaves = 8;  // waves per workgroup
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// Work split.  A wave scores TW tokens (at most 8 query tiles, held in registers) against
+// TPW key tiles; the SPLIT = ceil(M / TW) waves that share a key range sit in the same
+// workgroup, KW = 8 / SPLIT ranges per workgroup, KW * TPW contiguous key tiles in all.
+//
+// Key path: the key cache is row-major [L, 128], but the MFMA wants lane (r, g) to hold
+// 32 bytes of key r -- a strided read (16 rows per instruction) that measured ~2 us
+// slower over 16 MB than contiguous 1 KB reads.  So the workgroup reads its key tiles
+// contiguously into LDS (16-byte chunk c of row r stored at chunk position c ^ (r & 7):
+// the MFMA-layout reads are then free of bank conflicts), in PH phases that are all
+// requested at kernel start; phase p is computed while the later phases still arrive.
+// Query tiles (in MFMA fragment order), folded head weights and key scales are staged
+// in LDS by the same loads.  Every loop is unrolled with compile-time trip counts, all
+// loads are unconditional (indices clamped), and scores stay in registers until the
+// end, so no wait covers a later load or a store.
+template <int M, int H, int TW, int TPW>
+struct IdxShape {
+  static constexpr int TPT = H / 16;              // query tiles per token
+  static constexpr int QT = M * TPT;              // query tiles
+  static constexpr int QTW = TW * TPT;            // query tiles per wave
+  static constexpr int SPLIT = (M + TW - 1) / TW; // waves per key range
+  static constexpr int KW = kIdxWaves / SPLIT;    // key ranges per workgroup
+  static constexpr int PH = TPW >= 2 ? 2 : 1;     // key phases
+  static constexpr int TPP = TPW / PH;            // tiles per range per phase
+  static constexpr int PT = KW * TPP;             // tiles per phase (workgroup)
+  static constexpr int NT = KW * TPW;             // key tiles per workgroup
+  static constexpr int THREADS = kIdxWaves * 64;
+  static constexpr int QCH = QT * 128;            // 16-byte query chunks
+  static constexpr int QPT = (QCH + THREADS - 1) / THREADS;
+  static constexpr int KPT = (PT * 128 + THREADS - 1) / THREADS;  // key chunks per thread per phase
+  static constexpr int KSPT = (NT * 16 + THREADS - 1) / THREADS;  // key scales per thread
+  // LDS carve-up (bytes)
+  static constexpr int Q_OFF = 0;
+  static constexpr int WQ_OFF = Q_OFF + QPT * THREADS * 16;
+  static constexpr int KS_OFF = WQ_OFF + THREADS * 4;
+  static constexpr int K_OFF = KS_OFF + KSPT * THREADS * 4;
+  static constexpr int K_BYTES = KPT * THREADS * 16;  // one phase buffer
+  static constexpr int LDS = K_OFF + PH * K_BYTES;
+  static_assert(kIdxWaves % SPLIT == 0 && TW <= 4 && QT * 16 <= THREADS, "work split");
+};
+
+template <int M, int H, int TW, int TPW>
 __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ q_s, int q_s_per_head,
     const uint8_t* __restrict__ k, const float* __restrict__ k_s, const uint16_t* __restrict__ w,
-    float* __restrict__ logits, int L, int64_t ld, int64_t cur_pos, int n_tiles, int tiles_per_wave) {
-  constexpr int TPT = H / 16;   // query tiles per token
-  constexpr int QT = M * TPT;   // query tiles
-  const int lane = threadIdx.x & 63;
-  const int wave_global = blockIdx.x * kIdxWaves + (threadIdx.x >> 6);
+    float* __restrict__ logits, int L, int64_t ld, int64_t cur_pos, int n_tiles) {
+  using S = IdxShape<M, H, TW, TPW>;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int t_begin = wave_global * tiles_per_wave;
+  const int t0 = (wave % S::SPLIT) * TW;  // first token of this wave
+  const int rr = wave / S::SPLIT;         // key range of this wave
+  const int wg_tile = blockIdx.x * S::NT; // first key tile of the workgroup
 
-  auto load_keys = [&](int tile) -> v8i {
-    const int key = tile * 16 + r;
-    return key < L ? load_kblock_stream(k + static_cast<size_t>(key) * kBlock, g) : zero_v8i();
+  // ---- all global loads, issued together
+  // query chunk d of the LDS image (fragment order): tile d / 128, piece (d / 64) % 2,
+  // lane d % 64 -> row 16 qt + l % 16, 16-byte piece 4 p + l / 16 of that row
+  uint4 qv[S::QPT];
+#pragma unroll
+  for (int u = 0; u < S::QPT; ++u) {
+    const int d = min(tid + u * S::THREADS, S::QCH - 1);
+    const int qt = d >> 7, pp = (d >> 6) & 1, l = d & 63;
+    qv[u] = reinterpret_cast<const uint4*>(q)[((qt * 16 + (l & 15)) << 3) + pp * 4 + (l >> 4)];
+  }
+  const int wrow = min(tid, S::QT * 16 - 1);
+  const float wqv = bf16_to_f32(w[wrow]) * q_s[q_s_per_head ? wrow : wrow / H];
+  float ksv[S::KSPT];
+#pragma unroll
+  for (int u = 0; u < S::KSPT; ++u) {
+    const int e = tid + u * S::THREADS;  // key e % 16 of workgroup tile e / 16
+    const int key = min(min(wg_tile + e / 16, n_tiles - 1) * 16 + (e & 15), L - 1);
+    ksv[u] = k_s[key];
+  }
+  // key chunk c of phase p: phase tile pt = c / 128 (range pt / TPP, its tile
+  // p * TPP + pt % TPP), row (c / 8) % 16, 16-byte chunk c % 8 -- contiguous 1 KB reads
+  auto key_src = [&](int p, int c) {
+    const int pt = min(c >> 7, S::PT - 1);
+    const int tile = min(wg_tile + (pt / S::TPP) * TPW + p * S::TPP + pt % S::TPP, n_tiles - 1);
+    const int64_t byte = static_cast<int64_t>(tile) * 2048 + (c & 127) * 16;
+    return reinterpret_cast<const u32x4v*>(k + min(byte, static_cast<int64_t>(L) * kBlock - 16));
   };
-  // the first key tile is in flight while the workgroup stages the queries
-  v8i kb_next = t_begin < n_tiles ? load_keys(t_begin) : zero_v8i();
+  u32x4v kv[S::PH][S::KPT];
+#pragma unroll
+  for (int p = 0; p < S::PH; ++p)
+#pragma unroll
+    for (int u = 0; u < S::KPT; ++u) kv[p][u] = __builtin_nontemporal_load(key_src(p, tid + u * S::THREADS));
 
-  // stage the queries and the folded head weights w[t,h] * q_s once per workgroup
-  __shared__ __attribute__((aligned(16))) uint8_t q_lds[QT * 16 * kBlock];
-  __shared__ __attribute__((aligned(16))) float wq_lds[QT * 16];
-  for (int i = threadIdx.x; i < QT * 16 * kBlock / 16; i += kIdxWaves * 64)
-    reinterpret_cast<uint4*>(q_lds)[i] = reinterpret_cast<const uint4*>(q)[i];
-  for (int row = threadIdx.x; row < QT * 16; row += kIdxWaves * 64)
-    wq_lds[row] = bf16_to_f32(w[row]) * (q_s_per_head ? q_s[row] : q_s[row / H]);
+  // ---- stage queries, weights, key scales and key phase 0
+  uint4* q_lds = reinterpret_cast<uint4*>(smem + S::Q_OFF);
+  float* wq_lds = reinterpret_cast<float*>(smem + S::WQ_OFF);
+  float* ks_lds = reinterpret_cast<float*>(smem + S::KS_OFF);
+  auto key_lds = [&](int p) { return smem + S::K_OFF + p * S::K_BYTES; };
+  auto put_keys = [&](int p) {
+#pragma unroll
+    for (int u = 0; u < S::KPT; ++u) {
+      const int c = tid + u * S::THREADS;  // chunks past the phase land in the padding
+      const int row = (c >> 3) & 15, ch = c & 7;
+      *reinterpret_cast<u32x4v*>(key_lds(p) + (c >> 7) * 2048 + row * 128 + ((ch ^ (row & 7)) << 4)) = kv[p][u];
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < S::QPT; ++u) q_lds[tid + u * S::THREADS] = qv[u];
+  wq_lds[tid] = wqv;
+#pragma unroll
+  for (int u = 0; u < S::KSPT; ++u) ks_lds[tid + u * S::THREADS] = ksv[u];
+  put_keys(0);
   __syncthreads();
-  if (t_begin >= n_tiles) return;
-  const int t_end = min(n_tiles, t_begin + tiles_per_wave);
 
-  v8i qa[QT];  // query tiles (A operands), resident for the whole kernel
+  // ---- this wave's query tiles (A operands) and head weights; tokens past M (a short
+  //      last group) repeat token M-1 and are not stored
+  v8i qa[S::QTW];
+  float4 wq[S::QTW];
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) qa[qt] = load_kblock(q_lds + (qt * 16 + r) * kBlock, g);
+  for (int j = 0; j < S::QTW; ++j) {
+    const int qt = min(t0 + j / S::TPT, M - 1) * S::TPT + j % S::TPT;
+    const uint4 lo = q_lds[qt * 128 + lane];
+    const uint4 hi = q_lds[qt * 128 + 64 + lane];
+    qa[j] = v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+                static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+    wq[j] = *reinterpret_cast<const float4*>(wq_lds + qt * 16 + 4 * g);
+  }
 
-  for (int tile = t_begin; tile < t_end; ++tile) {
-    const v8i kbv = kb_next;
-    if (tile + 1 < t_end) kb_next = load_keys(tile + 1);
-    const int key = tile * 16 + r;
-    const float ks = key < L ? k_s[key] : 0.f;
-    float part[M];
+  float out[TPW];  // lane group g < TW: token t0 + g of key r
 #pragma unroll
-    for (int t = 0; t < M; ++t) {
-      float acc = 0.f;
+  for (int p = 0; p < S::PH; ++p) {
+    if (p > 0) {  // the next phase's keys have (mostly) arrived while this one computed
+      put_keys(p);
+      __syncthreads();
+    }
 #pragma unroll
-      for (int i = 0; i < TPT; ++i) {
-        const int qt = t * TPT + i;
-        const v4f c = mfma_16x16x128_fp8(qa[qt], kbv);
-        const float4 wq = *reinterpret_cast<const float4*>(wq_lds + qt * 16 + 4 * g);
-        acc = __builtin_fmaf(fmaxf(c[0], 0.f), wq.x, acc);
-        acc = __builtin_fmaf(fmaxf(c[1], 0.f), wq.y, acc);
-        acc = __builtin_fmaf(fmaxf(c[2], 0.f), wq.z, acc);
-        acc = __builtin_fmaf(fmaxf(c[3], 0.f), wq.w, acc);
+    for (int ii = 0; ii < S::TPP; ++ii) {
+      const int i = p * S::TPP + ii;
+      const uint8_t* tile = key_lds(p) + (rr * S::TPP + ii) * 2048 + r * 128;
+      const uint4 lo = *reinterpret_cast<const uint4*>(tile + ((g ^ (r & 7)) << 4));
+      const uint4 hi = *reinterpret_cast<const uint4*>(tile + (((g + 4) ^ (r & 7)) << 4));
+      const v8i kt = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+                      static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+      // all MFMAs of the tile first, into separate results, then the epilogue
+      v4f c[S::QTW];
+#pragma unroll
+      for (int j = 0; j < S::QTW; ++j) c[j] = mfma_16x16x128_fp8(qa[j], kt);
+      const float ksc = ks_lds[(rr * TPW + i) * 16 + r];
+      float score[TW];
+#pragma unroll
+      for (int t = 0; t < TW; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int jj = 0; jj < S::TPT; ++jj) {
+          const int j = t * S::TPT + jj;
+          acc = __builtin_fmaf(relu(c[j][0]), wq[j].x, acc);
+          acc = __builtin_fmaf(relu(c[j][1]), wq[j].y, acc);
+          acc = __builtin_fmaf(relu(c[j][2]), wq[j].z, acc);
+          acc = __builtin_fmaf(relu(c[j][3]), wq[j].w, acc);
+        }
+        // lanes r, r+16, r+32, r+48 hold the 4 partial head sums of key r: sum them with
+        // the gfx950 lane-swap instructions (VALU, no LDS round trip)
+        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
+        const float y = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
+        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+        score[t] = (__uint_as_float(s16[0]) + __uint_as_float(s16[1])) * ksc;
       }
-      part[t] = acc;
-    }
-    // lanes r, r+16, r+32, r+48 hold the 4 partial head sums of key r: sum them with
-    // the gfx950 lane-swap instructions (VALU, no LDS round trip)
-    float score[M];
+      float v = score[0];
 #pragma unroll
-    for (int t = 0; t < M; ++t) {
-      const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[t]), __float_as_uint(part[t]), false, false);
-      const float y = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
-      const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-      score[t] = (__uint_as_float(s16[0]) + __uint_as_float(s16[1])) * ks;
+      for (int tt = 1; tt < TW; ++tt)
+        if (tt == g) v = score[tt];
+      out[i] = v;
     }
-    // lane group g stores tokens g, g+4, ...: a 64-byte row segment per token
+  }
+
+  // lane group g stores token t0 + g: a 64-byte row segment per tile
+  const int tok = t0 + g;
+  const int t_begin = wg_tile + rr * TPW;
 #pragma unroll
-    for (int t0 = 0; t0 < M; t0 += 4) {
-      const int t = t0 + g;
-      if (t < M && key < L) {
-        float v = score[0];
-#pragma unroll
-        for (int tt = 1; tt < M; ++tt)
-          if (tt == t) v = score[tt];
-        if (static_cast<int64_t>(key) > cur_pos + t) v = -__builtin_inff();
-        logits[static_cast<int64_t>(t) * ld + key] = v;
-      }
-    }
+  for (int i = 0; i < TPW; ++i) {
+    const int key = (t_begin + i) * 16 + r;
+    if (g < TW && tok < M && t_begin + i < n_tiles && key < L)
+      logits[static_cast<int64_t>(tok) * ld + key] = static_cast<int64_t>(key) > cur_pos + tok ? -__builtin_inff() : out[i];
   }
 }
 
@@ -109,12 +214,40 @@ __global__ void fill_masked_kernel(float* __restrict__ logits, int M, int64_t ld
   logits[t * ld + c] = -__builtin_inff();
 }
 
+constexpr int kIdxMaxWaves = 2048;  // 8 per CU: beyond that a wave takes more key tiles
+
+template <int M, int H, int TW, int TPW>
+static int launch_indexer_t(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
+                            const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
+                            int L, int64_t ld, int64_t cur_pos, int n_tiles) {
+  using S = IdxShape<M, H, TW, TPW>;
+  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, TW, TPW>);
+  if (S::LDS > 64 * 1024) {
+    const int rc = allow_dynamic_lds(fn, S::LDS, "indexer");
+    if (rc) return rc;
+  }
+  const dim3 grid(static_cast<unsigned>(cdiv(n_tiles, static_cast<int64_t>(S::NT))));
+  hipLaunchKernelGGL((indexer_kernel<M, H, TW, TPW>), grid, dim3(kIdxWaves * 64), S::LDS, st, q, q_s, per_head, k,
+                     k_s, w, logits, L, ld, cur_pos, n_tiles);
+  return check_launch("indexer");
+}
+
 template <int M, int H>
-static void launch_indexer(dim3 grid, hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
-                           const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
-                           int L, int64_t ld, int64_t cur_pos, int n_tiles, int tpw) {
-  hipLaunchKernelGGL((indexer_kernel<M, H>), grid, dim3(kIdxWaves * 64), 0, st, q, q_s, per_head, k, k_s, w,
-                     logits, L, ld, cur_pos, n_tiles, tpw);
+static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
+                          const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
+                          int L, int64_t ld, int64_t cur_pos, int n_tiles) {
+  constexpr int TPT = H / 16;
+  constexpr int TW = (8 / TPT < M) ? 8 / TPT : M;  // tokens per wave: <= 8 query tiles
+  constexpr int SPLIT = (M + TW - 1) / TW;
+  // smallest tiles-per-wave that keeps the grid within 8 waves per CU
+  int tpw = 1;
+  while (tpw < 8 && static_cast<int64_t>(n_tiles) * SPLIT > static_cast<int64_t>(kIdxMaxWaves) * tpw) tpw *= 2;
+  switch (tpw) {
+    case 1: return launch_indexer_t<M, H, TW, 1>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 2: return launch_indexer_t<M, H, TW, 2>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 4: return launch_indexer_t<M, H, TW, 4>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    default: return launch_indexer_t<M, H, TW, 8>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+  }
 }
 
 }  // namespace tl
@@ -140,17 +273,12 @@ extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_
     const int64_t n = (L - visible) * M;
     hipLaunchKernelGGL(fill_masked_kernel, dim3(cdiv(n, 256)), dim3(256), 0, st, logits, (int)M, ld, visible, L);
   }
-  // 4 key tiles (64 keys, 8 KB) per wave at 128K keys: 2048 waves = 2 per SIMD, one
-  // 8-wave workgroup per CU (the kernel uses ~244 VGPRs at M*H = 256)
-  const int tpw = static_cast<int>(cdiv(n_tiles, 2048) < 2 ? 2 : cdiv(n_tiles, 2048));
-  const int waves = static_cast<int>(cdiv(n_tiles, tpw));
-  const dim3 grid(static_cast<unsigned>(cdiv(waves, kIdxWaves)));
   const uint8_t* q = (const uint8_t*)q_fp8;
   const uint8_t* k = (const uint8_t*)k_fp8;
   const uint16_t* w = (const uint16_t*)w_bf16;
   const int Li = static_cast<int>(L);
 #define TL_IDX(MM, HH) \
-  if (M == MM && H == HH) { launch_indexer<MM, HH>(grid, st, q, q_s, q_s_per_head, k, k_s, w, logits, Li, ld, cur_pos, n_tiles, tpw); return check_launch("indexer"); }
+  if (M == MM && H == HH) return launch_indexer<MM, HH>(st, q, q_s, q_s_per_head, k, k_s, w, logits, Li, ld, cur_pos, n_tiles);
   TL_IDX(1, 64) TL_IDX(2, 64) TL_IDX(3, 64) TL_IDX(4, 64)
   TL_IDX(1, 32) TL_IDX(2, 32) TL_IDX(3, 32) TL_IDX(4, 32) TL_IDX(5, 32) TL_IDX(6, 32) TL_IDX(7, 32) TL_IDX(8, 32)
 #undef TL_IDX
