@@ -69,6 +69,11 @@ GEMM_CASES = [
     (17, 512, 1024),
     (64, 1024, 2048),
     (256, 512, 1024),
+    (64, 2048, 7168),   # per-row-tile kernel, 4 token tiles, split-K
+    (128, 2048, 7168),  # tiled kernel (M > 64) with split-K
+    (32, 1152, 2048),
+    (200, 400, 2048),   # 25 row tiles: a partly empty last 128-row group
+    (100, 7168, 1024),
 ]
 
 
@@ -138,7 +143,7 @@ def test_fp8_gemm_rejects_bad_shapes(cuda):
         K.fp8_gemm(a, torch.zeros(4, 1, device=cuda), a, torch.zeros(1, 1, device=cuda))
 
 
-@pytest.mark.parametrize("M,N,Kd", [(4, 576, 7168), (4, 18432, 7168), (2, 7168, 2048)])
+@pytest.mark.parametrize("M,N,Kd", [(4, 576, 7168), (4, 18432, 7168), (2, 7168, 2048), (64, 2048, 7168), (128, 2048, 7168)])
 def test_fp8_gemm_split_k_repeatable(cuda, M, N, Kd):
     """The cross-workgroup split-K reduction must give bit-identical results on every
     call (a stale or missing partial would show up as a changed output)."""

@@ -24,6 +24,10 @@
 //     is chosen so the grid covers the 256 CUs evenly; the last workgroup of a row tile
 //     (agent-scope counter and agent-scope atomic partials) sums the fp32 partials in slice
 //     order, so results are deterministic.
+#include <algorithm>
+#include <type_traits>
+#include <utility>
+
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
@@ -249,31 +253,278 @@ __global__ __launch_bounds__(256) void pack_tile_major_kernel(const uint8_t* __r
   reinterpret_cast<uint4*>(P)[chunk] = *reinterpret_cast<const uint4*>(W + static_cast<size_t>(row) * K + col);
 }
 
+// ---------------------------------------------------------------- M > 64: tiled
+// For M > 64 tokens the activation blocks are no longer small next to the weights: a
+// wave that reads them from L1/L2 for each of its token tiles moves up to 4x the weight
+// bytes through the texture path.  Here a workgroup of 8 waves covers 128 rows (one
+// 16-row tile per wave) x all TT token tiles over a slice of K blocks:
+//   * activations (MFMA fragment order) and their scales are staged in LDS by the whole
+//     workgroup in chunks of KC = 16 / TT K blocks (32 KB), double-buffered and loaded
+//     one chunk ahead -- one barrier per chunk;
+//   * each wave streams its weight fragments through a ring of kTiledDepth buffers that
+//     runs on across chunk boundaries, so a barrier never drains the weight stream;
+//   * full chunks issue unconditional loads only (exact wait counts); the last chunks of
+//     a slice guard the weight fetches, so no fragment is read twice.
+// Split-K slices are reduced as in fp8_gemm_kernel (partials + last-arriver, in slice
+// order, deterministic).
+// static_for<N>(f): f(std::integral_constant<int, 0>{}) ... f(<N-1>) -- compile-time loop
+template <int... I, class F>
+__device__ __attribute__((always_inline)) inline void static_for_impl(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
+  static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+constexpr int kTiledWaves = 8;
+constexpr int kTiledDepth = 4;
+constexpr int kTiledChunkBytes = 32 * 1024;
+
+template <int TT>
+struct TiledShape {
+  static constexpr int THREADS = kTiledWaves * 64;
+  static constexpr int KC = 16 / TT >= 1 ? 16 / TT : 1;   // K blocks per chunk
+  static_assert(KC % kTiledDepth == 0 || kTiledDepth % KC == 0, "ring slots must be static");
+  static constexpr int XCH = KC * TT * 128;                // 16-byte chunks per chunk
+  static constexpr int XPT = (XCH + THREADS - 1) / THREADS;
+  static constexpr int XBUF = XPT * THREADS * 16;          // bytes per buffer (padded)
+  static constexpr int SCN = KC * TT * 16;                 // activation scales per chunk
+  static constexpr int SPT = (SCN + THREADS - 1) / THREADS;
+  static constexpr int SBUF = SPT * THREADS;               // floats per buffer (padded)
+  static constexpr int LDS = 2 * XBUF + 2 * SBUF * 4;
+};
+
+// dynamic LDS of fp8_gemm_tiled_kernel<TT>
+template <int TT>
+constexpr int tiled_lds_bytes() { return TiledShape<TT>::LDS; }
+
+template <int TT, bool PACKED>
+__global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, uint16_t* __restrict__ C, float* __restrict__ partial,
+    uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
+  using S = TiledShape<TT>;
+  constexpr int KC = S::KC, D = kTiledDepth, THREADS = S::THREADS;
+  extern __shared__ __attribute__((aligned(16))) uint8_t tiled_smem[];
+  __shared__ uint32_t last_flag;
+  const int KB = K >> 7;
+  const int NT = N >> 4;
+  const int ksplit = gridDim.y, ks = blockIdx.y;
+  const int kb_begin = ks * kb_per_split;
+  const int n = max(0, min(KB, kb_begin + kb_per_split) - kb_begin);  // K blocks in this slice
+  const int nch = (n + KC - 1) / KC;                                  // chunks
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int rt = min(static_cast<int>(blockIdx.x) * kTiledWaves + wave, NT - 1);  // rows past N: not stored
+  const bool row_ok = static_cast<int>(blockIdx.x) * kTiledWaves + wave < NT;
+  const uint8_t* brow = B + static_cast<size_t>(rt * 16 + r) * K;
+  const float* bs_row = Bs + static_cast<size_t>(rt >> 3) * KB;
+
+  // ---- activation chunks: chunk c covers K blocks kb_begin + c*KC + j, j < KC.  LDS
+  // image chunk d: block j = d / (TT*128), token tile tt = (d / 128) % TT, piece
+  // (d / 64) % 2, lane d % 64 -> token 16 tt + l % 16 (clamped), 16-byte piece 4 p + l / 16
+  u32x4 xr[S::XPT];  // ext-vector type: a HIP uint4 struct copy would stay in scratch
+  float sr[S::SPT];
+  auto x_issue = [&](int c) __attribute__((always_inline)) {  // unconditional, indices clamped
+    static_for<S::XPT>([&](auto ut) __attribute__((always_inline)) {
+      constexpr int u = decltype(ut)::value;
+      const int d = min(tid + u * THREADS, S::XCH - 1);
+      const int j = d / (TT * 128), tt = (d >> 7) % TT, pp = (d >> 6) & 1, l = d & 63;
+      const int kb = kb_begin + min(c * KC + j, n - 1);
+      const int tok = min(tt * 16 + (l & 15), M - 1);
+      xr[u] = *reinterpret_cast<const u32x4*>(A + static_cast<size_t>(tok) * K + kb * kBlock + pp * 64 + (l >> 4) * 16);
+    });
+    static_for<S::SPT>([&](auto ut) __attribute__((always_inline)) {
+      constexpr int u = decltype(ut)::value;
+      const int e = min(tid + u * THREADS, S::SCN - 1);  // scale e: block e / (TT*16), token e % (TT*16)
+      const int kb = kb_begin + min(c * KC + e / (TT * 16), n - 1);
+      sr[u] = As[static_cast<size_t>(min(e % (TT * 16), M - 1)) * KB + kb];
+    });
+  };
+  auto x_put = [&](int buf) __attribute__((always_inline)) {  // unconditional writes (padding absorbs the surplus)
+    u32x4* xl = reinterpret_cast<u32x4*>(tiled_smem + buf * S::XBUF);
+    float* sl = reinterpret_cast<float*>(tiled_smem + 2 * S::XBUF) + buf * S::SBUF;
+    static_for<S::XPT>([&](auto ut) __attribute__((always_inline)) { xl[tid + decltype(ut)::value * THREADS] = xr[decltype(ut)::value]; });
+    static_for<S::SPT>([&](auto ut) __attribute__((always_inline)) {
+      constexpr int u = decltype(ut)::value;
+      const int e = tid + u * THREADS;
+      sl[e] = (e % (TT * 16)) < M ? sr[u] : 0.f;  // tokens past M contribute 0
+    });
+  };
+
+  // ---- weight ring: item i = K block kb_begin + i
+  v8i wr[D];
+  float bsr[D];
+  // slot = i % D, always passed as a compile-time value (a runtime index would put the
+  // ring in scratch memory)
+  auto w_fetch = [&](int i, auto slot_tag) __attribute__((always_inline)) {
+    constexpr int slot = decltype(slot_tag)::value;
+    const int kb = kb_begin + min(i, n - 1);
+    wr[slot] = PACKED ? load_packed_fragment(B + packed_fragment(rt, kb, NT), lane)
+                      : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
+    bsr[slot] = bs_row[kb];
+  };
+
+  v4f acc[TT];
+#pragma unroll
+  for (int tt = 0; tt < TT; ++tt) acc[tt] = v4f{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](auto slot_tag, int buf, int j) __attribute__((always_inline)) {  // chunk block j of buffer buf
+    constexpr int slot = decltype(slot_tag)::value;
+    const u32x4* xl = reinterpret_cast<const u32x4*>(tiled_smem + buf * S::XBUF) + j * TT * 128;
+    const float* sl = reinterpret_cast<const float*>(tiled_smem + 2 * S::XBUF) + buf * S::SBUF + j * TT * 16;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const u32x4 lo = xl[tt * 128 + lane];
+      const u32x4 hi = xl[tt * 128 + 64 + lane];
+      const v8i xb = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+                      static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+      acc[tt] += mfma_16x16x128_fp8(wr[slot], xb) * (bsr[slot] * sl[tt * 16 + r]);
+      if ((tt & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the operand reads in flight
+    }
+  };
+
+  if (n > 0) {
+    // prologue: chunk 0 into LDS buffer 0, chunk 1 into registers, the first D-1 weights
+    x_issue(0);
+    x_put(0);
+    x_issue(1);
+    static_for<D - 1>([&](auto i) __attribute__((always_inline)) { w_fetch(decltype(i)::value, i); });
+    // one chunk: stage chunk c+1 (registers -> LDS), request chunk c+2, then its KC
+    // items.  CC = c % CPI is compile-time, so every ring slot is.  SAFE: every weight
+    // fetch of the chunk is inside the slice (no guard needed).
+    auto chunk = [&](int c, auto cc_tag, auto safe_tag) __attribute__((always_inline)) {
+      constexpr int CC = decltype(cc_tag)::value;
+      constexpr bool SAFE = decltype(safe_tag)::value;
+      __syncthreads();   // chunk c-1 is done everywhere: its buffer may be refilled
+      x_put((c + 1) & 1);
+      x_issue(c + 2);
+      static_for<KC>([&](auto jt) __attribute__((always_inline)) {
+        constexpr int j = decltype(jt)::value;
+        const int i = c * KC + j;
+        const auto cur = std::integral_constant<int, (CC * KC + j) % D>{};
+        const auto nxt = std::integral_constant<int, (CC * KC + j + D - 1) % D>{};
+        if (SAFE) {
+          w_fetch(i + D - 1, nxt);
+          compute(cur, c & 1, j);
+        } else if (i < n) {
+          if (i + D - 1 < n) w_fetch(i + D - 1, nxt);
+          compute(cur, c & 1, j);
+        }
+      });
+    };
+    __syncthreads();  // chunk 0 visible
+    // CPI chunks per loop step, unrolled, so that item i's ring slot i % D is a
+    // compile-time index (CPI * KC is a multiple of D)
+    constexpr int CPI = KC >= D ? 1 : D / KC;
+    int c = 0;
+    // a step is safe when its last fetch, item (c+CPI)*KC + D - 2, is inside the slice
+    for (; (c + CPI) * KC + D - 2 < n; c += CPI)
+      static_for<CPI>([&](auto cc) __attribute__((always_inline)) { chunk(c + decltype(cc)::value, cc, std::true_type{}); });
+    for (; c < nch; c += CPI)
+      static_for<CPI>([&](auto cc) __attribute__((always_inline)) {
+        if (c + decltype(cc)::value < nch) chunk(c + decltype(cc)::value, cc, std::false_type{});
+      });
+  }
+
+  // lane holds output rows rt*16 + 4g + j (j = 0..3) of token tt*16 + r
+  const int ncol = rt * 16 + 4 * g;
+  if (ksplit == 1) {
+    if (row_ok) {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const int t = tt * 16 + r;
+        if (t < M) *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(acc[tt]);
+      }
+    }
+    return;
+  }
+  // split-K: agent-scope partials, then the last slice of this row group sums them
+  if (row_ok) {
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = tt * 16 + r;
+      if (t < M) {
+        float* dst = partial + (static_cast<size_t>(ks) * M + t) * N + ncol;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) __hip_atomic_store(dst + j, acc[tt][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // every wave's partials are complete before the counter moves
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&counters[blockIdx.x], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = prev == static_cast<uint32_t>(ksplit - 1);
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  if (row_ok) {
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = tt * 16 + r;
+      if (t < M) {
+        v4f s = {0.f, 0.f, 0.f, 0.f};
+        for (int q0 = 0; q0 < ksplit; q0 += 8) {
+          v4f v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int q = q0 + u < ksplit ? q0 + u : ksplit - 1;
+            const float* src = partial + (static_cast<size_t>(q) * M + t) * N + ncol;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[u][j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (q0 + u < ksplit) s += v[u];
+        }
+        *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(s);
+      }
+    }
+  }
+  if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct GemmPlan {
+  bool tiled;  // M > 64: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
-  int row_tiles;
+  int row_groups;  // grid.x: 16-row tiles (GEMV) or 128-row groups (tiled)
   int waves;
 };
 
-// K split.  Wide layers (>= 512 row tiles, i.e. >= 2 workgroups per CU) run unsplit:
-// measured on MI355X, the split's extra round trips (partial store, counter, reload)
-// cost more than the better CU balance buys.  Narrow layers take the smallest split
-// giving >= 1024 workgroups (4 per CU), preferring a grid that is a whole multiple of
-// the 256 CUs, with slices of whole K groups, never leaving a slice empty.
-static GemmPlan plan_gemm(int64_t N, int64_t K) {
+// K split.  GEMV (M <= 16): wide layers (>= 512 row tiles, i.e. >= 2 workgroups per CU)
+// run unsplit: measured on MI355X, the split's extra round trips (partial store, counter,
+// reload) cost more than the better CU balance buys.  Narrow layers take the smallest
+// split giving >= 1024 workgroups (4 per CU), preferring a grid that is a whole multiple
+// of the 256 CUs, with slices of whole K groups, never leaving a slice empty.
+// Tiled (M > 64; measured faster than the per-row-tile kernel from M = 128 on, slower at
+// M = 32 and 64): the smallest split giving >= 512 workgroups (2 per CU) with slices of
+// at least 8 K blocks.
+static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
+  p.tiled = M > 64;
+  if (p.tiled) {
+    p.row_groups = static_cast<int>(cdiv(N / 16, kTiledWaves));
+    int s = static_cast<int>(cdiv(512, p.row_groups));
+    s = std::max(1, std::min(s, KB / 8));
+    p.kb_per_split = static_cast<int>(cdiv(KB, s));
+    p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
+    p.waves = kTiledWaves;
+    return p;
+  }
   const int groups = static_cast<int>(cdiv(KB, kGroup));
-  p.row_tiles = static_cast<int>(N / 16);
+  p.row_groups = static_cast<int>(N / 16);
   int s = 1;
-  if (p.row_tiles < 512) {
-    int smin = static_cast<int>(cdiv(1024, p.row_tiles));
+  if (p.row_groups < 512) {
+    int smin = static_cast<int>(cdiv(1024, p.row_groups));
     if (smin > groups) smin = groups;
     if (smin < 1) smin = 1;
     s = smin;
     for (int c = smin; c <= 2 * smin && c <= groups; ++c) {
-      if ((static_cast<int64_t>(p.row_tiles) * c) % 256 == 0) { s = c; break; }
+      if ((static_cast<int64_t>(p.row_groups) * c) % 256 == 0) { s = c; break; }
     }
   }
   p.kb_per_split = static_cast<int>(cdiv(groups, s)) * kGroup;
@@ -292,25 +543,36 @@ constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 template <bool PACKED>
 static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, const float* Bs,
                        uint16_t* C, int M, int N, int K, void* workspace, hipStream_t st) {
-  const GemmPlan p = plan_gemm(N, K);
+  const GemmPlan p = plan_gemm(M, N, K);
   uint32_t* counters = p.ksplit > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
   float* partial = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
-  const dim3 grid(p.row_tiles, p.ksplit);
+  const dim3 grid(p.row_groups, p.ksplit);
   const int per = p.kb_per_split;
+  if (p.tiled) {
+    auto launch = [&](auto tt_tag) -> int {
+      constexpr int TT = decltype(tt_tag)::value;
+      const void* fn = reinterpret_cast<const void*>(fp8_gemm_tiled_kernel<TT, PACKED>);
+      if (tiled_lds_bytes<TT>() > 60 * 1024) {
+        const int rc = allow_dynamic_lds(fn, tiled_lds_bytes<TT>(), "fp8_gemm");
+        if (rc) return rc;
+      }
+      hipLaunchKernelGGL((fp8_gemm_tiled_kernel<TT, PACKED>), grid, dim3(kTiledWaves * 64), tiled_lds_bytes<TT>(), st,
+                         A, As, B, Bs, C, partial, counters, M, N, K, per);
+      return check_launch("fp8_gemm");
+    };
+    if (M <= 128) return launch(std::integral_constant<int, 8>{});
+    return launch(std::integral_constant<int, 16>{});
+  }
 #define TL_GEMM_LAUNCH(MT, W) \
   hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, C, partial, counters, M, N, K, per)
   if (p.waves == 8) {
     if (M <= 16) TL_GEMM_LAUNCH(1, 8);
     else if (M <= 32) TL_GEMM_LAUNCH(2, 8);
-    else if (M <= 64) TL_GEMM_LAUNCH(4, 8);
-    else if (M <= 128) TL_GEMM_LAUNCH(8, 4);
-    else TL_GEMM_LAUNCH(16, 4);
+    else TL_GEMM_LAUNCH(4, 8);
   } else {
     if (M <= 16) TL_GEMM_LAUNCH(1, 4);
     else if (M <= 32) TL_GEMM_LAUNCH(2, 4);
-    else if (M <= 64) TL_GEMM_LAUNCH(4, 4);
-    else if (M <= 128) TL_GEMM_LAUNCH(8, 4);
-    else TL_GEMM_LAUNCH(16, 4);
+    else TL_GEMM_LAUNCH(4, 4);
   }
 #undef TL_GEMM_LAUNCH
   return check_launch("fp8_gemm");
@@ -340,7 +602,7 @@ using namespace tl;
 
 extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock || M > 256) return 0;
-  const GemmPlan p = plan_gemm(N, K);
+  const GemmPlan p = plan_gemm(M, N, K);
   if (p.ksplit == 1) return 0;
   return kCounterBytes + static_cast<size_t>(p.ksplit) * M * N * sizeof(float);
 }
