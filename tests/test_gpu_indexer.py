@@ -73,6 +73,8 @@ def _assert_topk_set(idx, scores, valid, k, rel_gap=1e-3):
     (4, 5000, 2048, 4996),
     (2, 3000, 512, 100),          # valid lengths 101, 102 < k: all + -1 padding
     (3, 9000, 1024, 4000),
+    (2, 65536, 8192, 65534),      # 4 chunks x k = 32768 candidates: the stage-B limit
+    (2, 49160, 2048, 49157),      # last chunk holds only 8 valid columns
 ])
 def test_topk_rows_vs_oracle(cuda, rows, L, k, base):
     g = synth.gen(rows + L + k)
@@ -94,6 +96,29 @@ def test_topk_ties_take_lowest_indices(cuda):
     out = topk_rows(x.to(cuda), L - 1, k).cpu()[0]
     want = sorted(list(range(7000, 7100)) + [i for i in range(L) if not 7000 <= i < 7100][: k - 100])
     assert out.tolist() == want
+
+
+def test_topk_ties_across_chunks(cuda):
+    """Ties at the threshold spread over several 16K-column chunks: the selection takes
+    every clear winner, then the lowest-column ties of the whole row, in ascending order."""
+    L, k = 50000, 2048
+    x = torch.zeros(1, L)
+    winners = list(range(100, L, 167))[:300]  # spread over all 4 chunks
+    x[0, winners] = 3.0
+    out = topk_rows(x.to(cuda), L - 1, k).cpu()[0]
+    ties = [i for i in range(L) if i not in set(winners)][: k - len(winners)]
+    assert out.tolist() == sorted(winners + ties)
+
+
+def test_topk_repeatable(cuda):
+    """The cross-workgroup handoff re-arms itself: repeated calls give the same set."""
+    g = synth.gen(77)
+    x = torch.randn(4, 131072, generator=g).to(cuda)
+    first = topk_rows(x, 131068, 2048)
+    outs = [topk_rows(x, 131068, 2048) for _ in range(20)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o, first)
 
 
 def test_topk_accurate_reference_contract(cuda):
