@@ -17,13 +17,14 @@
 //     each wave-wide load reads 1 KB of consecutive memory.  Packing is done once at
 //     weight-load time (tl_fp8_pack_weight), like the reference's per-op weight
 //     converters.  Measured on MI355X: packed fragments stream ~25% faster.
-//   * One weight fragment in flight per wave (U = 1) and 4-8 waves per workgroup: on
-//     this memory system deeper per-wave prefetch lowers achieved bandwidth.
-//   * Work split: a workgroup owns one 16-row tile and a slice of K blocks; its waves
-//     interleave over the slice and are summed through LDS in a fixed order.  The K split
-//     is chosen so the grid covers the 256 CUs evenly; the last workgroup of a row tile
-//     (agent-scope counter and agent-scope atomic partials) sums the fp32 partials in slice
-//     order, so results are deterministic.
+//   * M <= 64 (fp8_gemm_kernel): a workgroup owns one 16-row tile and a slice of K blocks;
+//     its 4-8 waves interleave over the slice, each with the next block's operands in
+//     flight (two buffers in ping-pong; deeper rings measured no faster), and are summed
+//     through LDS in a fixed order.  The K split is chosen so the grid covers the 256 CUs
+//     evenly; the last workgroup of a row tile (agent-scope counter and agent-scope atomic
+//     partials) sums the fp32 partials in slice order, so results are deterministic.
+//   * M > 64 (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks staged
+//     in LDS (see below).
 #include <algorithm>
 #include <type_traits>
 #include <utility>
