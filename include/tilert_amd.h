@@ -152,8 +152,9 @@ int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
  * row has fewer than k valid columns, all of them, then -1.  The selected set is exactly
  * torch.topk's (ops/topk.py:128-143) up to the choice among exact ties, which is
  * lowest-index-first here.  1 <= k <= 8192.  workspace: tl_topk_workspace_bytes(rows,
- * ld, k) bytes, ZERO-FILLED before first use and left zeroed by every call; calls sharing
- * it must be ordered.  Replaces topk_accurate_op (ops/topk.py:62-109). */
+ * ld, k) bytes, ZERO-FILLED before first use and left zeroed by every call (the state
+ * that must be zero has fixed offsets, so calls of any shapes may share one workspace);
+ * calls sharing it must be ordered.  Replaces topk_accurate_op (ops/topk.py:62-109). */
 size_t tl_topk_workspace_bytes(int64_t rows, int64_t ld, int64_t k);
 int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64_t valid_base, int64_t k,
                  int32_t* out, void* workspace, size_t workspace_bytes, void* stream);

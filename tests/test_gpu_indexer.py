@@ -121,6 +121,20 @@ def test_topk_repeatable(cuda):
         assert torch.equal(o, first)
 
 
+def test_topk_workspace_shared_across_shapes(cuda):
+    """One workspace serves calls of different shapes in any order: the state that must
+    stay zero sits at fixed offsets, so no call's candidates land on another's counters."""
+    g = synth.gen(91)
+    shapes = [(2, 65536, 8192), (4, 131072, 2048), (1, 20000, 512), (6, 40000, 1024), (2, 65536, 8192)]
+    for rows, L, k in shapes:
+        x = torch.randn(rows, L, generator=g)
+        out = topk_rows(x.to(cuda), L - rows, k).cpu()
+        valid = [L - rows + 1 + i for i in range(rows)]
+        want = ref.topk_rows(x, valid, k)
+        for i in range(rows):
+            assert torch.equal(out[i].sort().values, want[i].sort().values), (rows, L, k, i)
+
+
 def test_topk_accurate_reference_contract(cuda):
     g = synth.gen(3)
     x = torch.randn(1, 4, 8192, generator=g)

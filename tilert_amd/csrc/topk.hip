@@ -2,54 +2,85 @@
 // is torch.topk, :128-143), as ONE kernel with one cross-workgroup barrier and one handoff.
 //
 // Scores map to order-preserving 32-bit keys (larger score = larger key).  A row is cut
-// into 16K-column chunks, one 1024-thread workgroup each, which load their keys once and
-// keep them in registers (16 contiguous columns per thread).
-//   Stage 1 (every chunk): a histogram of the keys' top 11 bits in LDS, published with
-//     agent-scope stores; the row's chunks meet at a barrier (bounded spin), every chunk
-//     sums all partials and finds the digit d0 holding the row's k-th largest key and how
-//     many keys lie above it.  Each chunk then publishes its keys with digit >= d0 -- the
-//     only ones that can be selected -- as (key, column) pairs in ascending column order
-//     (typically ~2k per row in all).
-//   Stage 2 (the row's last chunk to finish, found with an agent-scope counter): two more
-//     radix passes (11 and 10 bits) over the candidates of digit d0 give the k-th largest
-//     key T; every candidate > T plus the lowest-column candidates == T until k are taken
-//     are written in ascending column order.  Candidates stay in registers when they fit
-//     (<= 8 per thread); otherwise they are streamed in batches, so any input is exact.
-// The set is exact and deterministic, ties included.  Two radix rounds that needed a
-// cross-workgroup exchange each are replaced by workgroup-local passes over the few
-// candidates: measured on MI355X, each exchange round costs several microseconds.
+// into chunks of 256 * PT columns, one 256-thread workgroup each (PT contiguous columns
+// per thread, kept in registers).  Small workgroups keep the LDS histogram's atomic
+// traffic per CU low: keys bunch into a few bins (sign, exponent and two mantissa bits),
+// and same-bin LDS atomics serialise.
+//   Stage 1 (every chunk): a histogram of the keys' top 11 bits in LDS; its non-zero bins
+//     are added into its group's copy of the row histogram with agent-scope atomics.  The
+//     row's last chunk to arrive (two-level counter) sums the copies, finds the digit d0
+//     holding the row's k-th largest key and how many keys lie above it, and broadcasts
+//     both; the other chunks wait for the word (bounded spin).  Each chunk then publishes
+//     its keys with digit >= d0 -- the only ones that can be selected -- as (key, column)
+//     pairs in ascending column order.
+//   Stage 2 (the row's last chunk to publish, found with a second two-level counter):
+//     radix passes (11, then 10 bits) over the candidates of digit d0 give the k-th
+//     largest key T, stopping early when the threshold digit's whole bin is needed; every
+//     candidate above T plus the lowest-column candidates equal to it until k are taken
+//     are written in ascending column order.  Candidates are read coalesced in batches of
+//     4096 and stay in registers when one batch holds them; otherwise every pass streams
+//     the batches again, so any input is exact.  The last chunk re-arms the counters.
+// Scans use DPP row shifts and row broadcasts inside a wave (no LDS round trips) and one
+// LDS exchange across the four waves.
+// The set is exact and deterministic, ties included.  Measured on MI355X, the cost is a
+// chain of device-scope round trips (~0.25 us each when uncontended; same-address atomics
+// serialise at tens of ns each, hence the groups), not bandwidth.
 //
-// The barrier needs the row's workgroups co-resident: the launch is at most one workgroup
-// per CU (<= 256 workgroups, checked on the host) and the kernel is the only work on its
-// stream; the wait is bounded (about a second) so a wave can never hang.
+// The barrier needs a launch's workgroups co-resident: a launch holds at most 256
+// workgroups (larger inputs are launched in groups of rows), and the wait is bounded
+// (about a second) so a wave can never hang.
 //
 // Rows are the topk_accurate samples: row i considers columns [0, valid_base + 1 + i).
+
+#include <algorithm>
 
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
 namespace tl {
 
-constexpr int kTkThreads = 1024;
-constexpr int kTkPerThread = 16;                      // 4 float4 loads per thread
-constexpr int kTkChunk = kTkThreads * kTkPerThread;   // 16384 columns per workgroup
+constexpr int kTkThreads = 256;
+constexpr int kTkWaves = kTkThreads / 64;
 constexpr int kBins = 2048;                           // widest digit: 11 bits
+constexpr int kBinsPerThread = kBins / kTkThreads;    // 8
 constexpr int kMaxK = 8192;
-constexpr int kMaxChunks = 16;
-constexpr int kMaxCols = kMaxChunks * kTkChunk;       // 262144
-constexpr int kMaxGroups = 256;                       // one workgroup per CU at most
-constexpr int kCandPerThread = 8;                     // stage-2 register batch per thread
+constexpr int kMaxCols = 262144;
+constexpr int kMaxGroups = 256;                       // workgroups per launch
+constexpr int kMaxChunks = 256;                       // per row
+constexpr int kCandPerThread = 16;                    // stage-2 register batch per thread
 constexpr int kCandBatch = kTkThreads * kCandPerThread;
 constexpr uint32_t kSpinLimit = 1u << 22;             // x s_sleep(8): ~1 s
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4t __attribute__((ext_vector_type(4)));
+
+// The workspace starts with a fixed state region -- per launch slot (blockIdx.y, at most
+// 256 rows per launch): arrival counters, the broadcast word and the row histograms --
+// that must be zero when a call starts and is left zero by every call.  Its offsets do
+// not depend on the problem shape, so calls of any shapes can share one workspace without
+// one call's candidates landing on another call's state.
+//
+// Same-address device-scope atomics serialise (tens of ns each), so a row's chunks are
+// split into G = min(8, chunks) groups (chunk % G): arrivals count per group first and the
+// last of a group bumps the row counter; the histogram has one copy per group; the
+// broadcast word one replica per group.
+constexpr int kSlots = kMaxGroups;
+constexpr int kGroups = 8;
+constexpr int kBufferRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
+constexpr int kCachePolicySc1 = 16;           // buffer access cache policy: sc1
+constexpr size_t kCounterBytes = 32768;
+constexpr size_t kStateBytes = kCounterBytes + static_cast<size_t>(kSlots) * kBins * sizeof(uint32_t);
 
 struct TopkWs {
-  uint32_t* arrive;  // [rows] barrier arrivals, zero between calls
-  uint32_t* done;    // [rows] chunks finished with stage 1, zero between calls
-  uint32_t* count;   // [rows][chunks] candidates published per chunk
-  uint32_t* part;    // [rows][chunks][kBins] pass-0 partial histograms
-  uint64_t* cand;    // [rows][chunks][kTkChunk] (key << 32 | column)
+  uint32_t* arrive1;  // [kSlots][kGroups] chunks of a group past the histogram
+  uint32_t* arrive2;  // [kSlots] groups past the histogram
+  uint32_t* done1;    // [kSlots][kGroups] chunks of a group past the candidate publication
+  uint32_t* done2;    // [kSlots] groups past the candidate publication
+  uint32_t* bcast;    // [kSlots][kGroups] (1 << 31) | d0 << 13 | above0
+  uint32_t* hist;     // [kSlots][kBins] histograms of the top 11 bits: launch row y uses
+                      // slots y*chunks .. y*chunks + G - 1 (one per group)
+  uint32_t* count;    // [rows][chunks] candidates published per chunk
+  uint64_t* cand;     // [rows][chunks][chunk columns] (key << 32 | column)
 };
 
 __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -57,14 +88,15 @@ __host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_
 __host__ __device__ inline TopkWs carve(void* base, int64_t rows, int64_t chunks) {
   char* p = static_cast<char*>(base);
   TopkWs w;
-  w.arrive = reinterpret_cast<uint32_t*>(p);
-  p += align256(rows * sizeof(uint32_t));
-  w.done = reinterpret_cast<uint32_t*>(p);
-  p += align256(rows * sizeof(uint32_t));
+  w.arrive1 = reinterpret_cast<uint32_t*>(p);
+  w.arrive2 = w.arrive1 + kSlots * kGroups;
+  w.done1 = w.arrive2 + kSlots;
+  w.done2 = w.done1 + kSlots * kGroups;
+  w.bcast = w.done2 + kSlots;
+  w.hist = reinterpret_cast<uint32_t*>(p + kCounterBytes);
+  p += kStateBytes;
   w.count = reinterpret_cast<uint32_t*>(p);
   p += align256(rows * chunks * sizeof(uint32_t));
-  w.part = reinterpret_cast<uint32_t*>(p);
-  p += align256(rows * chunks * kBins * sizeof(uint32_t));
   w.cand = reinterpret_cast<uint64_t*>(p);
   return w;
 }
@@ -81,251 +113,383 @@ __device__ inline int row_valid(int row, int64_t valid_base, int64_t ld) {
   return static_cast<int>(n);
 }
 
-// Block-wide exclusive prefix sum over the 1024 threads (returns the block total too).
-__device__ inline uint32_t block_excl_scan(uint32_t v, uint32_t* s_waves, uint32_t& total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) s_waves[wave] = x;
-  __syncthreads();
-  uint32_t before = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kTkThreads / 64; ++w) {
-    const uint32_t s = s_waves[w];
-    before += w < wave ? s : 0u;
-    total += s;
-  }
-  __syncthreads();
-  return before + x - v;
+__device__ inline uint32_t ld_agent(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st_agent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Inclusive prefix sum over a wave's 64 lanes: Hillis-Steele inside each 16-lane row
+// (row_shr 1, 2, 4, 8; lanes shifted in from outside the row read 0), then the last lane
+// of rows 0 / 2 is added to rows 1 / 3 (row_bcast:15) and the last lane of row 1 to rows
+// 2 and 3 (row_bcast:31).
+__device__ inline uint32_t wave_incl_scan(uint32_t x) {
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false);
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false);
+  return x;
 }
 
 struct TopkShared {
   uint32_t h[kBins];
-  uint32_t waves[kTkThreads / 64];
-  uint32_t digit, above, flag;
+  uint32_t waves[2][kTkWaves];
+  uint32_t digit, above, dcount, flag;
   uint32_t offs[kMaxChunks + 1];
+  uint64_t stage[kCandBatch / 16 * 17];
 };
 
-// The digit (of nb bins, histogram in sh.h) holding the k_rem-th largest key, and how
-// many keys lie in the digits above it.  Thread j owns digits [nb - (j+1)*per, nb - j*per),
-// i.e. descending order across threads; one block scan finds the owner.
-__device__ inline void find_digit(uint32_t nb, uint32_t k_rem, TopkShared& sh, uint32_t& digit, uint32_t& above) {
-  const uint32_t per = nb / kTkThreads;  // 2 or 1
-  const uint32_t hi = nb - threadIdx.x * per;
+// Block-wide exclusive prefix sum over the 256 threads (and the block total).  The two
+// wave-total slots alternate between calls, so one barrier per scan suffices: a slot is
+// rewritten only after the next scan's barrier, which every reader of it has passed.
+__device__ inline uint32_t block_excl_scan(uint32_t v, TopkShared& sh, int& slot, uint32_t& total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t x = wave_incl_scan(v);
+  if (lane == 63) sh.waves[slot][wave] = x;
+  __syncthreads();
+  uint32_t before = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kTkWaves; ++w) {
+    const uint32_t s = sh.waves[slot][w];
+    before += w < wave ? s : 0u;
+    total += s;
+  }
+  slot ^= 1;
+  return before + x - v;
+}
+
+// The digit holding the k_rem-th largest key, and how many keys lie in the digits above
+// it.  Thread t holds the counts of digits hi-1, hi-2, ..., hi-PER (hi = nb - t*PER), so
+// thread order is descending digit order and one block scan finds the owner.
+template <int PER>
+__device__ inline void pick_digit(const uint32_t (&cnt)[PER], uint32_t hi, uint32_t k_rem, TopkShared& sh,
+                                  int& slot, uint32_t& digit, uint32_t& above, uint32_t& dcount) {
   uint32_t own = 0;
-  for (uint32_t b = hi - per; b < hi; ++b) own += sh.h[b];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) own += cnt[i];
   uint32_t total;
-  const uint32_t above_me = block_excl_scan(own, sh.waves, total);
-  if (above_me < k_rem && above_me + own >= k_rem) {
-    uint32_t a = above_me;
-    uint32_t d = hi - 1;
-    for (;; --d) {
-      if (a + sh.h[d] >= k_rem) break;
-      a += sh.h[d];
+  const uint32_t before = block_excl_scan(own, sh, slot, total);
+  if (before < k_rem && before + own >= k_rem) {
+    uint32_t a = before, d = hi - PER, dc = 0;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      if (!found && a + cnt[i] >= k_rem) {
+        d = hi - 1 - i;
+        dc = cnt[i];
+        found = true;
+      }
+      if (!found) a += cnt[i];
     }
     sh.digit = d;
     sh.above = a;
+    sh.dcount = dc;
   }
   __syncthreads();
   digit = sh.digit;
   above = sh.above;
-  __syncthreads();
+  dcount = sh.dcount;
 }
 
+// Two-level arrival (thread 0): true for the row's last chunk.  Group g = chunk % G holds
+// chunks g, g+G, ...; its last arrival bumps the row counter.
+__device__ inline bool arrive_last(uint32_t* level1, uint32_t* level2, int chunk, int chunks, int groups) {
+  const int g = chunk % groups;
+  const uint32_t gsize = static_cast<uint32_t>((chunks - 1 - g) / groups + 1);
+  const uint32_t p1 = __hip_atomic_fetch_add(&level1[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (p1 != gsize - 1) return false;
+  const uint32_t p2 = __hip_atomic_fetch_add(level2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return p2 == static_cast<uint32_t>(groups - 1);
+}
+
+__device__ inline void zero_bins(TopkShared& sh) {  // thread t clears bins 8t .. 8t+7
+  u32x4t* h4 = reinterpret_cast<u32x4t*>(sh.h) + threadIdx.x * 2;
+  const u32x4t z = {0u, 0u, 0u, 0u};
+  h4[0] = z;
+  h4[1] = z;
+}
+
+template <int PT>
 __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restrict__ logits, int64_t ld,
-                                                          int64_t valid_base, int k, TopkWs ws,
+                                                          int64_t valid_base, int k, int row0, TopkWs ws,
                                                           int32_t* __restrict__ out) {
+  constexpr int kChunk = kTkThreads * PT;
+  static_assert(PT % 4 == 0 && PT <= 32, "float4 loads, one mask bit per key");
   __shared__ TopkShared sh;
-  const int row = blockIdx.y;
+  int slot = 0;
+  const int row = row0 + static_cast<int>(blockIdx.y), y = blockIdx.y;
   const int chunks = gridDim.x, chunk = blockIdx.x;
   const int n = row_valid(row, valid_base, ld);
   int32_t* o = out + static_cast<int64_t>(row) * k;
   if (n <= k) {  // every valid column, then -1 padding (no barrier: the whole row exits)
-    const int64_t base = static_cast<int64_t>(chunk) * kTkChunk;
-    for (int64_t c = base + threadIdx.x; c < base + kTkChunk && c < k; c += kTkThreads)
-      o[c] = c < n ? static_cast<int32_t>(c) : -1;
+    const int base = chunk * kChunk;
+    for (int c = base + static_cast<int>(threadIdx.x); c < base + kChunk && c < k; c += kTkThreads)
+      o[c] = c < n ? c : -1;
     return;
   }
 
-  // ---- stage 1: this chunk's keys (16 contiguous columns per thread)
+  // ---- stage 1: this chunk's keys (PT contiguous columns per thread)
   const float* src = logits + static_cast<int64_t>(row) * ld;
-  const int64_t c0 = static_cast<int64_t>(chunk) * kTkChunk + static_cast<int64_t>(threadIdx.x) * kTkPerThread;
-  uint32_t key[kTkPerThread], vm = 0;
-  if (c0 + kTkPerThread <= n) {
-    f32x4 v[4];
+  const int c0 = chunk * kChunk + static_cast<int>(threadIdx.x) * PT;
+  uint32_t key[PT], vm = 0;
+  if (c0 + PT <= n) {
+    f32x4 v[PT / 4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + c0 + 4 * i);
+    for (int i = 0; i < PT / 4; ++i) v[i] = *reinterpret_cast<const f32x4*>(src + c0 + 4 * i);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < PT / 4; ++i)
 #pragma unroll
       for (int j = 0; j < 4; ++j) key[4 * i + j] = order_key(v[i][j]);
-    vm = 0xffffu;
+    vm = PT == 32 ? 0xffffffffu : ((1u << PT) - 1u);
   } else {
 #pragma unroll
-    for (int i = 0; i < kTkPerThread; ++i) {
+    for (int i = 0; i < PT; ++i) {
       const bool ok = c0 + i < n;
-      key[i] = ok ? order_key(src[c0 + i]) : 0u;
+      key[i] = ok ? order_key(src[ok ? c0 + i : 0]) : 0u;
       vm |= ok ? (1u << i) : 0u;
     }
   }
-  for (uint32_t b = threadIdx.x; b < kBins; b += kTkThreads) sh.h[b] = 0;
+  zero_bins(sh);
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kTkPerThread; ++i)
+  for (int i = 0; i < PT; ++i)
     if ((vm >> i) & 1u) atomicAdd(&sh.h[key[i] >> 21], 1u);
   __syncthreads();
-  uint32_t* part = ws.part + static_cast<size_t>(row) * chunks * kBins;
-  for (uint32_t b = threadIdx.x; b < kBins; b += kTkThreads)
-    __hip_atomic_store(&part[static_cast<size_t>(chunk) * kBins + b], sh.h[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // this chunk's non-zero bins into its group's histogram (thread t: bins 8t .. 8t+7)
+  const int groups = min(kGroups, chunks), grp = chunk % groups;
+  uint32_t* rh = ws.hist + static_cast<int64_t>(y) * chunks * kBins;  // group g's at rh + g*kBins
+  {
+    const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h) + threadIdx.x * 2;
+    const u32x4t a = h4[0], b = h4[1];
+    const uint32_t hv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (hv[i])
+        __hip_atomic_fetch_add(&rh[grp * kBins + threadIdx.x * 8 + i], hv[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  // per-row barrier (bounded wait)
-  if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(&ws.arrive[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    for (uint32_t it = 0; it < kSpinLimit; ++it) {
-      if (__hip_atomic_load(&ws.arrive[row], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= static_cast<uint32_t>(chunks)) break;
-      __builtin_amdgcn_s_sleep(8);
+  if (threadIdx.x == 0) sh.flag = arrive_last(ws.arrive1 + y * kGroups, ws.arrive2 + y, chunk, chunks, groups);
+  __syncthreads();
+  // The row's last chunk to arrive sums the group histograms (thread t: digits hi-1 ..
+  // hi-8, hi = 2048 - 8t), finds d0, broadcasts (valid bit, d0, above0) and re-zeroes the
+  // histograms; the others wait for their group's replica of that word (bounded spin).
+  if (sh.flag) {
+    const uint32_t hi = kBins - threadIdx.x * kBinsPerThread;
+    // 16-byte loads that bypass the non-coherent cache level (sc1), as the agent-scope
+    // atomic loads do; every sub-histogram's atomics completed before its chunk arrived
+    const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(rh, 0, kGroups * kBins * 4, kBufferRsrcWord3);
+    u32x4t a[kGroups], b[kGroups];
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      const int off = (g < groups ? g : 0) * kBins * 4 + static_cast<int>(hi - 8) * 4;
+      a[g] = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, kCachePolicySc1);
+      b[g] = __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, kCachePolicySc1);
     }
+    uint32_t cnt[kBinsPerThread] = {};
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      if (g < groups) {
+        const uint32_t v[8] = {b[g].w, b[g].z, b[g].y, b[g].x, a[g].w, a[g].z, a[g].y, a[g].x};
+#pragma unroll
+        for (int i = 0; i < kBinsPerThread; ++i) cnt[i] += v[i];
+      }
+    }
+    uint32_t d, above, dc;
+    pick_digit(cnt, hi, static_cast<uint32_t>(k), sh, slot, d, above, dc);
+    if (threadIdx.x < static_cast<unsigned>(groups)) st_agent(&ws.bcast[y * kGroups + threadIdx.x], 0x80000000u | (d << 13) | above);
+    // re-zeroed after the broadcast: nothing reads them again before this kernel ends
+    const u32x4t z = {0u, 0u, 0u, 0u};
+    for (int g = 0; g < groups; ++g) {
+      u32x4t* p4 = reinterpret_cast<u32x4t*>(rh + g * kBins + hi - 8);
+      p4[0] = z;
+      p4[1] = z;
+    }
+  } else if (threadIdx.x == 0) {
+    uint32_t w = 0;
+    for (uint32_t it = 0; it < kSpinLimit; ++it) {
+      w = ld_agent(&ws.bcast[y * kGroups + grp]);
+      if (w >> 31) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+    sh.digit = (w >> 13) & (kBins - 1);
+    sh.above = w & 0x1fffu;
   }
   __syncthreads();
-  // every chunk's partial summed (batched agent-scope loads)
-  for (uint32_t b = threadIdx.x; b < kBins; b += kTkThreads) {
-    uint32_t v[kMaxChunks];
-#pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c)
-      v[c] = __hip_atomic_load(&part[static_cast<size_t>(c < chunks ? c : chunks - 1) * kBins + b], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t s = 0;
-#pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) s += c < chunks ? v[c] : 0u;
-    sh.h[b] = s;
-  }
-  __syncthreads();
-  uint32_t d0, above0;
-  find_digit(kBins, static_cast<uint32_t>(k), sh, d0, above0);
+  const uint32_t d0 = sh.digit, above0 = sh.above;
 
   // candidates: keys with digit >= d0, compacted in ascending column order
   uint32_t cbits = 0;
 #pragma unroll
-  for (int i = 0; i < kTkPerThread; ++i) cbits |= (((vm >> i) & 1u) && (key[i] >> 21) >= d0) ? (1u << i) : 0u;
+  for (int i = 0; i < PT; ++i) cbits |= (((vm >> i) & 1u) && (key[i] >> 21) >= d0) ? (1u << i) : 0u;
   uint32_t n_cand;
-  uint32_t pos = block_excl_scan(__builtin_popcount(cbits), sh.waves, n_cand);
-  uint64_t* cand = ws.cand + (static_cast<size_t>(row) * chunks + chunk) * kTkChunk;
+  uint32_t pos = block_excl_scan(__builtin_popcount(cbits), sh, slot, n_cand);
+  uint64_t* cand = ws.cand + (static_cast<int64_t>(row) * chunks + chunk) * kChunk;
 #pragma unroll
-  for (int i = 0; i < kTkPerThread; ++i)
+  for (int i = 0; i < PT; ++i)
     if ((cbits >> i) & 1u) {
       const uint64_t v = (static_cast<uint64_t>(key[i]) << 32) | static_cast<uint32_t>(c0 + i);
       __hip_atomic_store(cand + pos++, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  if (threadIdx.x == 0)
-    __hip_atomic_store(&ws.count[row * chunks + chunk], n_cand, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) st_agent(&ws.count[static_cast<int64_t>(row) * chunks + chunk], n_cand);
   __builtin_amdgcn_s_waitcnt(0);  // this chunk's candidates are complete before it reports
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&ws.done[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sh.flag = prev == static_cast<uint32_t>(chunks - 1);
-  }
+  if (threadIdx.x == 0) sh.flag = arrive_last(ws.done1 + y * kGroups, ws.done2 + y, chunk, chunks, groups);
   __syncthreads();
   if (!sh.flag) return;
 
-  // ---- stage 2 (the row's last chunk): the candidates, in ascending column order
-  if (threadIdx.x == 0) {
-    uint32_t acc = 0;
-    for (int c = 0; c < chunks; ++c) {
-      sh.offs[c] = acc;
-      acc += __hip_atomic_load(&ws.count[row * chunks + c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    for (int c = chunks; c <= kMaxChunks; ++c) sh.offs[c] = acc;
-    // every chunk of the row is past the barrier and has reported: re-arm both counters
-    __hip_atomic_store(&ws.arrive[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&ws.done[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // ---- stage 2 (the row's last chunk)
+  const uint64_t* rc = ws.cand + static_cast<int64_t>(row) * chunks * kChunk;
+  // offsets of every chunk's candidates (entries past the last chunk hold C)
+  uint32_t C;
+  {
+    const uint32_t cn = threadIdx.x < static_cast<unsigned>(chunks)
+                            ? ld_agent(&ws.count[static_cast<int64_t>(row) * chunks + threadIdx.x]) : 0u;
+    sh.offs[threadIdx.x] = block_excl_scan(cn, sh, slot, C);
+    if (threadIdx.x == 0) sh.offs[kMaxChunks] = C;
+    __syncthreads();
   }
-  __syncthreads();
-  const uint32_t C = sh.offs[chunks];
-  uint32_t offs[kMaxChunks + 1];  // in registers: the load addresses need no LDS round trips
-#pragma unroll
-  for (int c = 0; c <= kMaxChunks; ++c) offs[c] = sh.offs[c];
-  const uint64_t* rc = ws.cand + static_cast<size_t>(row) * chunks * kTkChunk;
-  // candidate j of batch b0: thread t holds j = b0 + t*32 + i (contiguous, in order)
+  int lg = 0;  // binary-search depth: smallest power of two >= chunks
+  while ((1 << lg) < chunks) ++lg;
+  // Candidate batches of 4096 in column order.  A batch is read coalesced (thread t loads
+  // j = b0 + 256 i + t), staged in LDS, and taken back as 16 contiguous candidates per
+  // thread (j = b0 + 16 t + i), so thread order is column order.  Rows padded to 17
+  // entries keep both LDS access patterns free of bank conflicts.
   uint64_t cv[kCandPerThread];
-  auto load_batch = [&](uint32_t b0) {
+  auto load_batch = [&](uint32_t b0) __attribute__((always_inline)) {
+    uint32_t j[kCandPerThread];
+    int c[kCandPerThread];
 #pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) {  // all loads issued before any is used
-      const uint32_t j = min(b0 + threadIdx.x * kCandPerThread + i, C - 1);
-      int c = 0;
-#pragma unroll
-      for (int cc = 1; cc < kMaxChunks; ++cc) c += (offs[cc] <= j && cc < chunks) ? 1 : 0;
-      cv[i] = __hip_atomic_load(rc + static_cast<size_t>(c) * kTkChunk + (j - offs[c]), __ATOMIC_RELAXED,
-                                __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < kCandPerThread; ++i) {
+      j[i] = min(b0 + i * kTkThreads + threadIdx.x, C - 1);
+      c[i] = 0;
     }
-  };
-  auto batch_mask = [&](uint32_t b0) {
+    // the largest chunk c with offs[c] <= j: chunks without candidates share their
+    // successor's offset, so they are stepped over
+    for (int sstep = lg - 1; sstep >= 0; --sstep) {
+#pragma unroll
+      for (int i = 0; i < kCandPerThread; ++i) {
+        const int nc = c[i] + (1 << sstep);  // <= 255: offs[] past the last chunk hold C > j
+        c[i] = sh.offs[nc] <= j[i] ? nc : c[i];
+      }
+    }
+    uint64_t v[kCandPerThread];
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i)
+      v[i] = __hip_atomic_load(rc + static_cast<int64_t>(c[i]) * kChunk + (j[i] - sh.offs[c[i]]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();  // the previous batch's staging reads are complete
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) {
+      const int e = i * kTkThreads + threadIdx.x;
+      sh.stage[(e >> 4) * 17 + (e & 15)] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kCandPerThread; ++i) cv[i] = sh.stage[threadIdx.x * 17 + i];
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < kCandPerThread; ++i) m |= (b0 + threadIdx.x * kCandPerThread + i < C) ? (1u << i) : 0u;
     return m;
   };
-  const bool resident = C <= static_cast<uint32_t>(kCandBatch);
-  if (resident) load_batch(0);
+  const uint32_t n_batches = (C + kCandBatch - 1) / kCandBatch;
+  const uint32_t m_res = load_batch(0);
+  // body(mask) over every candidate batch (the first one stays loaded)
+  auto for_batches = [&](auto&& body) __attribute__((always_inline)) {
+    for (uint32_t bi = 0; bi < n_batches; ++bi) {
+      uint32_t m = m_res;
+      if (n_batches > 1) m = load_batch(bi * kCandBatch);
+      body(m);
+    }
+  };
 
-  // two radix passes over the candidates of digit d0 (the rest are above it)
-  uint32_t prefix = d0;
+  // radix passes over the candidates of digit d0 (the rest are above it) until the
+  // threshold digit's whole bin is needed: then every key of that bin is taken
+  uint32_t prefix = d0, tshift = 21;
   uint32_t k_rem = static_cast<uint32_t>(k) - above0;
+  bool resolved = C == static_cast<uint32_t>(k);  // digit d0's whole bin is needed
+#pragma unroll
   for (int pass = 1; pass < 3; ++pass) {
+    if (resolved) break;
     const int shift = pass == 1 ? 10 : 0;
     const int width = pass == 1 ? 11 : 10;
-    const uint32_t nb = 1u << width;
-    for (uint32_t b = threadIdx.x; b < kBins; b += kTkThreads) sh.h[b] = 0;
+    zero_bins(sh);
     __syncthreads();
-    for (uint32_t b0 = 0; b0 < C; b0 += kCandBatch) {
-      if (!resident) load_batch(b0);
-      const uint32_t m = batch_mask(b0);
+    for_batches([&](uint32_t m) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < kCandPerThread; ++i) {
         const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32);
-        if (((m >> i) & 1u) && (kk >> (shift + width)) == prefix) atomicAdd(&sh.h[(kk >> shift) & (nb - 1)], 1u);
+        if (((m >> i) & 1u) && (kk >> (shift + width)) == prefix)
+          atomicAdd(&sh.h[(kk >> shift) & ((1u << width) - 1u)], 1u);
       }
-    }
+    });
     __syncthreads();
-    uint32_t d, above;
-    find_digit(nb, k_rem, sh, d, above);
+    uint32_t d, above, dc;
+    if (pass == 1) {  // 2048 digits, 8 per thread
+      const uint32_t hi = kBins - threadIdx.x * 8;
+      const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h + hi - 8);
+      const u32x4t a = h4[0], b = h4[1];
+      const uint32_t cnt[8] = {b.w, b.z, b.y, b.x, a.w, a.z, a.y, a.x};
+      pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
+    } else {  // 1024 digits, 4 per thread
+      const uint32_t hi = (kBins / 2) - threadIdx.x * 4;
+      const u32x4t a = *reinterpret_cast<const u32x4t*>(sh.h + hi - 4);
+      const uint32_t cnt[4] = {a.w, a.z, a.y, a.x};
+      pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
+    }
     prefix = (prefix << width) | d;
     k_rem -= above;
+    tshift = shift;
+    resolved = dc == k_rem;
   }
   const uint32_t T = prefix;
   const uint32_t need_eq = k_rem;
 
-  // emit: candidates > T, then == T in order until need_eq, in ascending column order
+  // emit: candidates above T, then those equal to T (compared on bits >= tshift) in
+  // column order until need_eq, all in ascending column order
   uint32_t base = 0, eq_base = 0;
-  for (uint32_t b0 = 0; b0 < C; b0 += kCandBatch) {
-    if (!resident) load_batch(b0);
-    const uint32_t m = batch_mask(b0);
+  for_batches([&](uint32_t m) __attribute__((always_inline)) {
     uint32_t n_eq = 0;
 #pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) n_eq += ((m >> i) & 1u) && static_cast<uint32_t>(cv[i] >> 32) == T;
+    for (int i = 0; i < kCandPerThread; ++i)
+      n_eq += ((m >> i) & 1u) && (static_cast<uint32_t>(cv[i] >> 32) >> tshift) == T;
     uint32_t eq_tot;
-    uint32_t eq_rank = eq_base + block_excl_scan(n_eq, sh.waves, eq_tot);
+    uint32_t eq_rank = eq_base + block_excl_scan(n_eq, sh, slot, eq_tot);
     uint32_t sel = 0;
 #pragma unroll
     for (int i = 0; i < kCandPerThread; ++i) {
-      const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32);
+      const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32) >> tshift;
       const bool valid = (m >> i) & 1u;
       const bool eq = valid && kk == T;
       sel |= ((valid && kk > T) || (eq && eq_rank < need_eq)) ? (1u << i) : 0u;
       eq_rank += eq;
     }
     uint32_t sel_tot;
-    uint32_t p = base + block_excl_scan(__builtin_popcount(sel), sh.waves, sel_tot);
+    uint32_t p = base + block_excl_scan(__builtin_popcount(sel), sh, slot, sel_tot);
 #pragma unroll
     for (int i = 0; i < kCandPerThread; ++i)
-      if ((sel >> i) & 1u) o[p++] = static_cast<int32_t>(static_cast<uint32_t>(cv[i]));
+      if ((sel >> i) & 1u) {
+        if (p < static_cast<uint32_t>(k)) o[p] = static_cast<int32_t>(static_cast<uint32_t>(cv[i]));
+        ++p;
+      }
     base += sel_tot;
     eq_base += eq_tot;
+  });
+  // every chunk is past the broadcast and has published its candidates: re-arm the row's
+  // counters (last, so that no wait on these stores delays the selection)
+  if (threadIdx.x < static_cast<unsigned>(groups)) {
+    st_agent(&ws.arrive1[y * kGroups + threadIdx.x], 0u);
+    st_agent(&ws.done1[y * kGroups + threadIdx.x], 0u);
+    st_agent(&ws.bcast[y * kGroups + threadIdx.x], 0u);
+  }
+  if (threadIdx.x == 0) {
+    st_agent(&ws.arrive2[y], 0u);
+    st_agent(&ws.done2[y], 0u);
   }
 }
 
@@ -333,14 +497,38 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
 
 using namespace tl;
 
-static int64_t topk_chunks(int64_t ld) { return cdiv(ld, kTkChunk); }
+namespace {
+
+// Columns per thread: 16 when every row of the call fits one launch that way (rows *
+// chunks <= 256; measured faster than 8 per thread at 4 x 128K), otherwise 32, and rows
+// are launched in groups.
+struct TopkPlan {
+  int pt, chunks, rows_per_launch;
+};
+
+TopkPlan plan_topk(int64_t rows, int64_t ld) {
+  TopkPlan p{32, 0, 0};
+  for (int pt : {16, 32}) {
+    const int64_t ch = cdiv(ld, static_cast<int64_t>(kTkThreads) * pt);
+    if (rows * ch <= kMaxGroups || pt == 32) {
+      p.pt = pt;
+      p.chunks = static_cast<int>(ch);
+      break;
+    }
+  }
+  p.rows_per_launch = static_cast<int>(std::min<int64_t>(rows, kMaxGroups / std::max(p.chunks, 1)));
+  return p;
+}
+
+}  // namespace
 
 extern "C" size_t tl_topk_workspace_bytes(int64_t rows, int64_t ld, int64_t k) {
   (void)k;
-  if (rows <= 0 || ld <= 0) return 0;
-  const int64_t chunks = topk_chunks(ld);
-  return 2 * align256(rows * 4) + align256(rows * chunks * 4) + align256(static_cast<size_t>(rows) * chunks * kBins * 4) +
-         static_cast<size_t>(rows) * chunks * kTkChunk * 8;
+  if (rows <= 0 || ld <= 0 || ld > kMaxCols) return 0;
+  const TopkPlan p = plan_topk(rows, ld);
+  const size_t chunk_cols = static_cast<size_t>(kTkThreads) * p.pt;
+  return kStateBytes + align256(static_cast<size_t>(rows) * p.chunks * 4) +
+         static_cast<size_t>(rows) * p.chunks * chunk_cols * 8;
 }
 
 extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64_t valid_base, int64_t k,
@@ -349,14 +537,23 @@ extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64
   if (k < 1 || k > kMaxK) { set_error("topk: k=%lld must be in [1, %d]", (long long)k, kMaxK); return kErrUnsupported; }
   if (ld > kMaxCols) { set_error("topk: ld=%lld > %d columns is not supported", (long long)ld, kMaxCols); return kErrUnsupported; }
   if (ld % 4) { set_error("topk: ld=%lld must be a multiple of 4 (16-byte rows)", (long long)ld); return kErrArg; }
-  const int64_t chunks = topk_chunks(ld);
-  if (rows * chunks > kMaxGroups) { set_error("topk: rows * ceil(ld/16384) = %lld exceeds %d co-resident workgroups", (long long)(rows * chunks), kMaxGroups); return kErrUnsupported; }
+  if (rows > (1 << 20)) { set_error("topk: rows=%lld exceeds %d", (long long)rows, 1 << 20); return kErrUnsupported; }
   if (!logits || !out) { set_error("topk: null pointer"); return kErrArg; }
   if (reinterpret_cast<uintptr_t>(logits) & 15) { set_error("topk: logits must be 16-byte aligned"); return kErrArg; }
   const size_t need = tl_topk_workspace_bytes(rows, ld, k);
   if (!workspace || workspace_bytes < need) { set_error("topk: workspace of %zu bytes required (got %zu)", need, workspace_bytes); return kErrArg; }
-  const TopkWs ws = carve(workspace, rows, chunks);
-  hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(rows)), dim3(kTkThreads),
-                     0, (hipStream_t)stream, logits, ld, valid_base, (int)k, ws, out);
-  return check_launch("topk");
+  const TopkPlan p = plan_topk(rows, ld);
+  if (p.chunks < 1 || p.chunks > kMaxChunks || p.rows_per_launch < 1) {
+    set_error("topk: internal plan error (chunks=%d)", p.chunks);
+    return kErrUnsupported;
+  }
+  const TopkWs ws = carve(workspace, rows, p.chunks);
+  auto kern = p.pt == 16 ? topk_kernel<16> : topk_kernel<32>;
+  for (int64_t r0 = 0; r0 < rows; r0 += p.rows_per_launch) {
+    const int nr = static_cast<int>(std::min<int64_t>(p.rows_per_launch, rows - r0));
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(p.chunks), static_cast<unsigned>(nr)), dim3(kTkThreads), 0,
+                       (hipStream_t)stream, logits, ld, valid_base, (int)k, static_cast<int>(r0), ws, out);
+    if (int rc = check_launch("topk")) return rc;
+  }
+  return kOk;
 }
