@@ -20,6 +20,7 @@
 // per-expert matrices: gate/up as w13 [E][2I rows (gate then up)][D], down as
 // w2 [E][D rows][I]; scales [E][2I/128][D/128] and [E][D/128][I/128].
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "../../include/tilert_amd.h"
@@ -33,6 +34,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups per CU)
 constexpr int kDownWaves = 8;       // down waves per workgroup
 constexpr int kDownSlots = 4;  // hit experts reduced together by the down kernel
+constexpr int kDownRedBytes = sizeof(float) * kDownWaves * kDownSlots * 4 * 64;  // cross-wave partials
+constexpr int kDownTermBytes = sizeof(float) * kDownSlots * 4 * 64;              // per-slot terms
 constexpr int kMaxLocalExperts = 64;
 
 typedef float v2f __attribute__((ext_vector_type(2)));
@@ -298,18 +301,23 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
 }
 
 // ------------------------------------------------------ down, LDS activations
-// Used when one hit expert's h rows [M, I] fit in 64 KB.  Hit experts are taken
-// `sb` at a time (sb * M * I * 2 <= 64 KB); the batch's h rows are staged in LDS and the
-// (slot, K block) items dealt round-robin to the waves are streamed kDnDepth ahead through
-// ring_pipeline, one fp32 accumulator per slot.  After the stream the same LDS holds the
-// cross-wave partials; wave 0 combines exactly as moe_down_kernel does.
-__global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
+// Used when one hit expert's h rows [M, I] fit in 64 KB.  A workgroup covers TPW 16-row
+// output tiles with 8 waves each, so the staged h rows serve TPW tiles.  Hit experts are
+// taken `sb` at a time (sb * M * I * 2 <= 64 KB); the batch's h rows are staged in LDS and
+// each tile's (slot, K block) items, dealt round-robin to its 8 waves, are streamed
+// kDnDepth ahead through ring_pipeline, one fp32 accumulator per slot.  After the stream
+// the same LDS holds the cross-wave partials: local wave j of a tile reduces slot j over
+// the tile's waves in order and rounds its weighted term to bf16 (the golden's per-term
+// rounding, as moe_down_kernel does); local wave 0 adds the terms in slot order.
+template <int TPW>
+__global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
     const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ topk_idx, const float* __restrict__ topk_w, int M, int topk, int e0,
     int n_local, int D, int I, int sb, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* hl = reinterpret_cast<uint16_t*>(smem);  // [sb][M][I] during the stream
   float(*red)[kDownSlots][4][64] = reinterpret_cast<float(*)[kDownSlots][4][64]>(smem);  // after it
+  float(*term)[kDownSlots][4][64] = reinterpret_cast<float(*)[kDownSlots][4][64]>(smem + TPW * kDownRedBytes);
   const int pairs = M * topk;
   const int my_e = lane_pair_expert(topk_idx, pairs, e0);
   const float my_w = lane_pair_weight(topk_w, pairs);
@@ -318,10 +326,11 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
   const int KB = I >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int tt = wave / kDownWaves, wl = wave % kDownWaves;           // tile in group, local wave
   const int r = lane & 15, g = lane >> 4;
   const bool tok = r < M;
   const int row = min(r, M - 1);
-  const int rt = blockIdx.x;
+  const int rt = blockIdx.x * TPW + tt;
   v4f yacc = {0.f, 0.f, 0.f, 0.f};
 
   for (int s0 = 0; s0 < n_hit; s0 += sb) {
@@ -331,16 +340,17 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
 #pragma unroll
     for (int j = 0; j < kDownSlots; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
     const int items = ns * KB;  // item = (slot it / KB, K block it % KB)
-    const int n = wave < items ? (items - wave + kDownWaves - 1) / kDownWaves : 0;
+    const int n = wl < items ? (items - wl + kDownWaves - 1) / kDownWaves : 0;
     struct Ops {
       v8i w;
       float sc;
     };
     Ops buf[kDnDepth];
+    float wj = 0.f;  // routing weight of (token r, slot s0 + wl): local wave j reduces slot j
     ring_pipeline(
         n, buf,
         [&](int i, Ops& o) {
-          const int it = wave + i * kDownWaves;
+          const int it = wl + i * kDownWaves;
           const int j = it / KB, kb = it - j * KB;
           const int e = nth_set_bit(mask, s0 + j);  // scalar bit arithmetic (no indexed array)
           const uint8_t* f = w2 + (static_cast<size_t>(e) * (D >> 4) + rt) * KB * 2048;
@@ -349,7 +359,7 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
           o.sc = load_f32_vector(sp + kb);
         },
         [&](int i, const Ops& o) {
-          const int it = wave + i * kDownWaves;
+          const int it = wl + i * kDownWaves;
           const int j = it / KB, kb = it - j * KB;
           const ActOperand xa = lds_act(hl + (j * M + row) * I + kb * kBlock, g);
 #pragma unroll
@@ -358,6 +368,8 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
         },
         [&] {  // the batch's h rows into LDS while the first weight fetches are in flight
           stage_commit(hl, stage_issue(h + static_cast<size_t>(s0) * M * I, h16), h16);
+          if (wl < ns)
+            wj = routing_weight(topk_idx, topk_w, my_e, my_w, pairs, topk, e0, r, tok, nth_set_bit(mask, s0 + wl));
           __syncthreads();
         });
     __syncthreads();  // every wave is done with hl before it becomes the partials
@@ -366,20 +378,24 @@ __global__ __launch_bounds__(kDownWaves * 64, 4) void moe_down_lds_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) red[wave][j][q][lane] = acc[j][q];
     __syncthreads();
-    if (wave == 0) {
-      for (int j = 0; j < ns; ++j) {
-        v4f t = {0.f, 0.f, 0.f, 0.f};
-        for (int w = 0; w < kDownWaves; ++w)
+    if (wl < ns) {
+      v4f t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int q = 0; q < 4; ++q) t[q] += red[w][j][q][lane];
-        const float wj = routing_weight(topk_idx, topk_w, my_e, my_w, pairs, topk, e0, r, tok, nth_set_bit(mask, s0 + j));
+      for (int w = 0; w < kDownWaves; ++w)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) yacc[q] += bf16_to_f32(f32_to_bf16(t[q] * wj));
-      }
+        for (int q = 0; q < 4; ++q) t[q] += red[tt * kDownWaves + w][wl][q][lane];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) term[tt][wl][q][lane] = bf16_to_f32(f32_to_bf16(t[q] * wj));
+    }
+    __syncthreads();
+    if (wl == 0) {
+      for (int j = 0; j < ns; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) yacc[q] += term[tt][j][q][lane];
     }
     __syncthreads();
   }
-  if (wave == 0 && tok) {
+  if (wl == 0 && tok) {
     uint16_t* dst = y + static_cast<size_t>(r) * D + rt * 16 + 4 * g;
     *reinterpret_cast<uint2*>(dst) =
         make_uint2(f32_to_bf16(yacc[0]) | (static_cast<uint32_t>(f32_to_bf16(yacc[1])) << 16),
@@ -626,13 +642,20 @@ extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, co
   const int64_t h_bytes = M * I * 2;  // one hit expert's h rows
   if (h_bytes <= kLdsActBytes && M * topk <= 64) {  // activations staged in LDS, sb hit experts per batch
     const int sb = static_cast<int>(std::min<int64_t>(kDownSlots, kLdsActBytes / h_bytes));
-    const size_t red_bytes = sizeof(float) * kDownWaves * kDownSlots * 4 * 64;
-    const size_t lds = std::max<size_t>(static_cast<size_t>(sb) * h_bytes, red_bytes);
-    rc = allow_dynamic_lds(reinterpret_cast<const void*>(moe_down_lds_kernel), kLdsActBytes, "moe_down_combine");
+    // two output tiles per workgroup when the tile count is even: the staged h serves both
+    auto launch = [&](auto tpw_tag) -> int {
+      constexpr int TPW = decltype(tpw_tag)::value;
+      const size_t lds = std::max<size_t>(static_cast<size_t>(sb) * h_bytes, TPW * (kDownRedBytes + kDownTermBytes));
+      const void* fn = reinterpret_cast<const void*>(moe_down_lds_kernel<TPW>);
+      const int rc2 = allow_dynamic_lds(fn, static_cast<int>(std::max<size_t>(lds, kLdsActBytes)), "moe_down_combine");
+      if (rc2) return rc2;
+      hipLaunchKernelGGL((moe_down_lds_kernel<TPW>), dim3(D / 16 / TPW), dim3(kDownWaves * 64 * TPW), lds,
+                         (hipStream_t)stream, (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w,
+                         (int)M, (int)topk, (int)expert_begin, (int)n_local, (int)D, (int)I, sb, (uint16_t*)y_bf16);
+      return 0;
+    };
+    rc = (D / 16) % 2 == 0 ? launch(std::integral_constant<int, 2>{}) : launch(std::integral_constant<int, 1>{});
     if (rc) return rc;
-    hipLaunchKernelGGL(moe_down_lds_kernel, dim3(D / 16), dim3(kDownWaves * 64), lds, (hipStream_t)stream,
-                       (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
-                       (int)expert_begin, (int)n_local, (int)D, (int)I, sb, (uint16_t*)y_bf16);
   } else {
     hipLaunchKernelGGL(moe_down_kernel, dim3(D / 16), dim3(kDownWaves * 64), 0, (hipStream_t)stream,
                        (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w, (int)M, (int)topk,
