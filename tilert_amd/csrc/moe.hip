@@ -186,6 +186,7 @@ __device__ inline ActOperand lds_act(const uint16_t* row_kblock, int g) {
 // issues a FIXED number of loads per thread (surplus threads reload the last chunk), so
 // the compiler's wait counts for the loads issued before it stay exact; stage_commit
 // writes the chunks to LDS once they have arrived.
+typedef __attribute__((address_space(3))) void* lds_ptr;
 constexpr int kStageChunks = 8;  // 64 KB with 512 threads
 struct Staged {
   u32x4 v[kStageChunks];
@@ -321,6 +322,17 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
   const int pairs = M * topk;
   const int my_e = lane_pair_expert(topk_idx, pairs, e0);
   const float my_w = lane_pair_weight(topk_w, pairs);
+  // The first batch's h rows (min(sb, n_local) slots: h holds n_local) are copied straight
+  // into LDS (global_load_lds, no registers) together with the routing loads, before the
+  // hit set is known; the copy is waited for just before the first compute.
+  const int pre16 = min(sb, n_local) * M * I / 8;
+  {
+    const int ln = threadIdx.x & 63;
+    for (int c0 = threadIdx.x - ln; c0 < pre16; c0 += blockDim.x)  // c0: this wave's first chunk
+      if (c0 + ln < pre16)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(h) + c0 + ln,
+                                         (lds_ptr)(smem + static_cast<size_t>(c0) * 16), 16, 0, 0);
+  }
   const uint64_t mask = lane_pairs_mask(my_e, n_local);
   const int n_hit = __builtin_popcountll(mask);
   const int KB = I >> 7;
@@ -367,9 +379,10 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
             if (jj == j) acc[jj] = mfma_block_bf16(o.w, o.sc, xa, acc[jj]);
         },
         [&] {  // the batch's h rows into LDS while the first weight fetches are in flight
-          stage_commit(hl, stage_issue(h + static_cast<size_t>(s0) * M * I, h16), h16);
+          if (s0 > 0) stage_commit(hl, stage_issue(h + static_cast<size_t>(s0) * M * I, h16), h16);
           if (wl < ns)
             wj = routing_weight(topk_idx, topk_w, my_e, my_w, pairs, topk, e0, r, tok, nth_set_bit(mask, s0 + wl));
+          if (s0 == 0) __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the direct copy has landed
           __syncthreads();
         });
     __syncthreads();  // every wave is done with hl before it becomes the partials
