@@ -75,6 +75,7 @@ def _assert_topk_set(idx, scores, valid, k, rel_gap=1e-3):
     (3, 9000, 1024, 4000),
     (2, 65536, 8192, 65534),      # 4 chunks x k = 32768 candidates: the stage-B limit
     (2, 49160, 2048, 49157),      # last chunk holds only 8 valid columns
+    (2, 131072, 4096, 131070),    # 4096 < candidates <= 8192: the 32-per-thread selection
 ])
 def test_topk_rows_vs_oracle(cuda, rows, L, k, base):
     g = synth.gen(rows + L + k)

@@ -18,7 +18,7 @@
 //     largest key T, stopping early when the threshold digit's whole bin is needed; every
 //     candidate above T plus the lowest-column candidates equal to it until k are taken
 //     are written in ascending column order.  Candidates are read coalesced in batches of
-//     4096 and stay in registers when one batch holds them; otherwise every pass streams
+//     8192 and stay in registers when one batch holds them; otherwise every pass streams
 //     the batches again, so any input is exact.  The last chunk re-arms the counters.
 // Scans use DPP row shifts and row broadcasts inside a wave (no LDS round trips) and one
 // LDS exchange across the four waves.
@@ -33,6 +33,7 @@
 // Rows are the topk_accurate samples: row i considers columns [0, valid_base + 1 + i).
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "../../include/tilert_amd.h"
@@ -47,7 +48,7 @@ constexpr int kMaxK = 8192;
 constexpr int kMaxCols = 262144;
 constexpr int kMaxGroups = 256;                       // workgroups per launch
 constexpr int kMaxChunks = 256;                       // per row
-constexpr int kCandPerThread = 16;                    // stage-2 register batch per thread
+constexpr int kCandPerThread = 32;                    // stage-2 register batch per thread
 constexpr int kCandBatch = kTkThreads * kCandPerThread;
 constexpr uint32_t kSpinLimit = 1u << 22;             // x s_sleep(8): ~1 s
 
@@ -139,7 +140,6 @@ struct TopkShared {
   uint32_t waves[2][kTkWaves];
   uint32_t digit, above, dcount, flag;
   uint32_t offs[kMaxChunks + 1];
-  uint64_t stage[kCandBatch / 16 * 17];
 };
 
 // Block-wide exclusive prefix sum over the 256 threads (and the block total).  The two
@@ -220,6 +220,7 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
   constexpr int kChunk = kTkThreads * PT;
   static_assert(PT % 4 == 0 && PT <= 32, "float4 loads, one mask bit per key");
   __shared__ TopkShared sh;
+  extern __shared__ uint64_t stage[];  // [kCandBatch / 32 * 33]: the stage-2 batch staging buffer
   int slot = 0;
   const int row = row0 + static_cast<int>(blockIdx.y), y = blockIdx.y;
   const int chunks = gridDim.x, chunk = blockIdx.x;
@@ -356,130 +357,141 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
   }
   int lg = 0;  // binary-search depth: smallest power of two >= chunks
   while ((1 << lg) < chunks) ++lg;
-  // Candidate batches of 4096 in column order.  A batch is read coalesced (thread t loads
-  // j = b0 + 256 i + t), staged in LDS, and taken back as 16 contiguous candidates per
-  // thread (j = b0 + 16 t + i), so thread order is column order.  Rows padded to 17
-  // entries keep both LDS access patterns free of bank conflicts.
-  uint64_t cv[kCandPerThread];
-  auto load_batch = [&](uint32_t b0) __attribute__((always_inline)) {
-    uint32_t j[kCandPerThread];
-    int c[kCandPerThread];
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) {
-      j[i] = min(b0 + i * kTkThreads + threadIdx.x, C - 1);
-      c[i] = 0;
-    }
-    // the largest chunk c with offs[c] <= j: chunks without candidates share their
-    // successor's offset, so they are stepped over
-    for (int sstep = lg - 1; sstep >= 0; --sstep) {
-#pragma unroll
-      for (int i = 0; i < kCandPerThread; ++i) {
-        const int nc = c[i] + (1 << sstep);  // <= 255: offs[] past the last chunk hold C > j
-        c[i] = sh.offs[nc] <= j[i] ? nc : c[i];
+  // CPT candidates per thread: 16 when the candidates fit one batch of 4096 (the common
+  // case, fewer registers and instructions), else 32 (batches of 8192).
+  auto select = [&](auto cpt_tag) __attribute__((always_inline)) {
+    constexpr int CPT = decltype(cpt_tag)::value;
+    constexpr int CB = kTkThreads * CPT;
+    // Candidate batches of CB = 256 * CPT in column order.  A batch is read coalesced
+    // (thread t loads j = b0 + 256 i + t), staged in LDS, and taken back as CPT contiguous
+    // candidates per thread (j = b0 + CPT t + i), so thread order is column order.  Rows
+    // padded to CPT + 1 entries keep both LDS access patterns free of bank conflicts.
+    uint64_t cv[CPT];
+    auto load_batch = [&](uint32_t b0) __attribute__((always_inline)) {
+      uint32_t j[CPT];
+      int c[CPT];
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        j[i] = min(b0 + i * kTkThreads + threadIdx.x, C - 1);
+        c[i] = 0;
       }
-    }
-    uint64_t v[kCandPerThread];
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i)
-      v[i] = __hip_atomic_load(rc + static_cast<int64_t>(c[i]) * kChunk + (j[i] - sh.offs[c[i]]), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();  // the previous batch's staging reads are complete
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) {
-      const int e = i * kTkThreads + threadIdx.x;
-      sh.stage[(e >> 4) * 17 + (e & 15)] = v[i];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) cv[i] = sh.stage[threadIdx.x * 17 + i];
-    uint32_t m = 0;
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) m |= (b0 + threadIdx.x * kCandPerThread + i < C) ? (1u << i) : 0u;
-    return m;
-  };
-  const uint32_t n_batches = (C + kCandBatch - 1) / kCandBatch;
-  const uint32_t m_res = load_batch(0);
-  // body(mask) over every candidate batch (the first one stays loaded)
-  auto for_batches = [&](auto&& body) __attribute__((always_inline)) {
-    for (uint32_t bi = 0; bi < n_batches; ++bi) {
-      uint32_t m = m_res;
-      if (n_batches > 1) m = load_batch(bi * kCandBatch);
-      body(m);
-    }
-  };
+      // the largest chunk c with offs[c] <= j: chunks without candidates share their
+      // successor's offset, so they are stepped over
+      for (int sstep = lg - 1; sstep >= 0; --sstep) {
+  #pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const int nc = c[i] + (1 << sstep);  // <= 255: offs[] past the last chunk hold C > j
+          c[i] = sh.offs[nc] <= j[i] ? nc : c[i];
+        }
+      }
+      uint64_t v[CPT];
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i)
+        v[i] = __hip_atomic_load(rc + static_cast<int64_t>(c[i]) * kChunk + (j[i] - sh.offs[c[i]]), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();  // the previous batch's staging reads are complete
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int e = i * kTkThreads + threadIdx.x;
+        stage[(e / CPT) * (CPT + 1) + (e % CPT)] = v[i];
+      }
+      __syncthreads();
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) cv[i] = stage[threadIdx.x * (CPT + 1) + i];
+      uint32_t m = 0;
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) m |= (b0 + threadIdx.x * CPT + i < C) ? (1u << i) : 0u;
+      return m;
+    };
+    const uint32_t n_batches = (C + CB - 1) / CB;
+    const uint32_t m_res = load_batch(0);
+    // body(mask) over every candidate batch (the first one stays loaded)
+    auto for_batches = [&](auto&& body) __attribute__((always_inline)) {
+      for (uint32_t bi = 0; bi < n_batches; ++bi) {
+        uint32_t m = m_res;
+        if (n_batches > 1) m = load_batch(bi * CB);
+        body(m);
+      }
+    };
 
-  // radix passes over the candidates of digit d0 (the rest are above it) until the
-  // threshold digit's whole bin is needed: then every key of that bin is taken
-  uint32_t prefix = d0, tshift = 21;
-  uint32_t k_rem = static_cast<uint32_t>(k) - above0;
-  bool resolved = C == static_cast<uint32_t>(k);  // digit d0's whole bin is needed
-#pragma unroll
-  for (int pass = 1; pass < 3; ++pass) {
-    if (resolved) break;
-    const int shift = pass == 1 ? 10 : 0;
-    const int width = pass == 1 ? 11 : 10;
-    zero_bins(sh);
-    __syncthreads();
+    // radix passes over the candidates of digit d0 (the rest are above it) until the
+    // threshold digit's whole bin is needed: then every key of that bin is taken
+    uint32_t prefix = d0, tshift = 21;
+    uint32_t k_rem = static_cast<uint32_t>(k) - above0;
+    bool resolved = C == static_cast<uint32_t>(k);  // digit d0's whole bin is needed
+  #pragma unroll
+    for (int pass = 1; pass < 3; ++pass) {
+      if (resolved) break;
+      const int shift = pass == 1 ? 10 : 0;
+      const int width = pass == 1 ? 11 : 10;
+      zero_bins(sh);
+      __syncthreads();
+      for_batches([&](uint32_t m) __attribute__((always_inline)) {
+  #pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+          const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32);
+          if (((m >> i) & 1u) && (kk >> (shift + width)) == prefix)
+            atomicAdd(&sh.h[(kk >> shift) & ((1u << width) - 1u)], 1u);
+        }
+      });
+      __syncthreads();
+      uint32_t d, above, dc;
+      if (pass == 1) {  // 2048 digits, 8 per thread
+        const uint32_t hi = kBins - threadIdx.x * 8;
+        const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h + hi - 8);
+        const u32x4t a = h4[0], b = h4[1];
+        const uint32_t cnt[8] = {b.w, b.z, b.y, b.x, a.w, a.z, a.y, a.x};
+        pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
+      } else {  // 1024 digits, 4 per thread
+        const uint32_t hi = (kBins / 2) - threadIdx.x * 4;
+        const u32x4t a = *reinterpret_cast<const u32x4t*>(sh.h + hi - 4);
+        const uint32_t cnt[4] = {a.w, a.z, a.y, a.x};
+        pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
+      }
+      prefix = (prefix << width) | d;
+      k_rem -= above;
+      tshift = shift;
+      resolved = dc == k_rem;
+    }
+    const uint32_t T = prefix;
+    const uint32_t need_eq = k_rem;
+
+    // emit: candidates above T, then those equal to T (compared on bits >= tshift) in
+    // column order until need_eq, all in ascending column order
+    uint32_t base = 0, eq_base = 0;
     for_batches([&](uint32_t m) __attribute__((always_inline)) {
-#pragma unroll
-      for (int i = 0; i < kCandPerThread; ++i) {
-        const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32);
-        if (((m >> i) & 1u) && (kk >> (shift + width)) == prefix)
-          atomicAdd(&sh.h[(kk >> shift) & ((1u << width) - 1u)], 1u);
+      uint32_t n_eq = 0;
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i)
+        n_eq += ((m >> i) & 1u) && (static_cast<uint32_t>(cv[i] >> 32) >> tshift) == T;
+      uint32_t eq_tot;
+      uint32_t eq_rank = eq_base + block_excl_scan(n_eq, sh, slot, eq_tot);
+      uint32_t sel = 0;
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32) >> tshift;
+        const bool valid = (m >> i) & 1u;
+        const bool eq = valid && kk == T;
+        sel |= ((valid && kk > T) || (eq && eq_rank < need_eq)) ? (1u << i) : 0u;
+        eq_rank += eq;
       }
+      uint32_t sel_tot;
+      uint32_t p = base + block_excl_scan(__builtin_popcount(sel), sh, slot, sel_tot);
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i)
+        if ((sel >> i) & 1u) {
+          if (p < static_cast<uint32_t>(k)) o[p] = static_cast<int32_t>(static_cast<uint32_t>(cv[i]));
+          ++p;
+        }
+      base += sel_tot;
+      eq_base += eq_tot;
     });
-    __syncthreads();
-    uint32_t d, above, dc;
-    if (pass == 1) {  // 2048 digits, 8 per thread
-      const uint32_t hi = kBins - threadIdx.x * 8;
-      const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h + hi - 8);
-      const u32x4t a = h4[0], b = h4[1];
-      const uint32_t cnt[8] = {b.w, b.z, b.y, b.x, a.w, a.z, a.y, a.x};
-      pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
-    } else {  // 1024 digits, 4 per thread
-      const uint32_t hi = (kBins / 2) - threadIdx.x * 4;
-      const u32x4t a = *reinterpret_cast<const u32x4t*>(sh.h + hi - 4);
-      const uint32_t cnt[4] = {a.w, a.z, a.y, a.x};
-      pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
-    }
-    prefix = (prefix << width) | d;
-    k_rem -= above;
-    tshift = shift;
-    resolved = dc == k_rem;
-  }
-  const uint32_t T = prefix;
-  const uint32_t need_eq = k_rem;
+  };
+  if (C <= static_cast<uint32_t>(kTkThreads * 16))
+    select(std::integral_constant<int, 16>{});
+  else
+    select(std::integral_constant<int, 32>{});
 
-  // emit: candidates above T, then those equal to T (compared on bits >= tshift) in
-  // column order until need_eq, all in ascending column order
-  uint32_t base = 0, eq_base = 0;
-  for_batches([&](uint32_t m) __attribute__((always_inline)) {
-    uint32_t n_eq = 0;
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i)
-      n_eq += ((m >> i) & 1u) && (static_cast<uint32_t>(cv[i] >> 32) >> tshift) == T;
-    uint32_t eq_tot;
-    uint32_t eq_rank = eq_base + block_excl_scan(n_eq, sh, slot, eq_tot);
-    uint32_t sel = 0;
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i) {
-      const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32) >> tshift;
-      const bool valid = (m >> i) & 1u;
-      const bool eq = valid && kk == T;
-      sel |= ((valid && kk > T) || (eq && eq_rank < need_eq)) ? (1u << i) : 0u;
-      eq_rank += eq;
-    }
-    uint32_t sel_tot;
-    uint32_t p = base + block_excl_scan(__builtin_popcount(sel), sh, slot, sel_tot);
-#pragma unroll
-    for (int i = 0; i < kCandPerThread; ++i)
-      if ((sel >> i) & 1u) {
-        if (p < static_cast<uint32_t>(k)) o[p] = static_cast<int32_t>(static_cast<uint32_t>(cv[i]));
-        ++p;
-      }
-    base += sel_tot;
-    eq_base += eq_tot;
-  });
   // every chunk is past the broadcast and has published its candidates: re-arm the row's
   // counters (last, so that no wait on these stores delays the selection)
   if (threadIdx.x < static_cast<unsigned>(groups)) {
@@ -549,9 +561,12 @@ extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64
   }
   const TopkWs ws = carve(workspace, rows, p.chunks);
   auto kern = p.pt == 16 ? topk_kernel<16> : topk_kernel<32>;
+  const int stage_bytes = kCandBatch / 32 * 33 * static_cast<int>(sizeof(uint64_t));
+  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), stage_bytes, "topk"))
+    return rc;
   for (int64_t r0 = 0; r0 < rows; r0 += p.rows_per_launch) {
     const int nr = static_cast<int>(std::min<int64_t>(p.rows_per_launch, rows - r0));
-    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(p.chunks), static_cast<unsigned>(nr)), dim3(kTkThreads), 0,
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(p.chunks), static_cast<unsigned>(nr)), dim3(kTkThreads), stage_bytes,
                        (hipStream_t)stream, logits, ld, valid_base, (int)k, static_cast<int>(r0), ws, out);
     if (int rc = check_launch("topk")) return rc;
   }
