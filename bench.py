@@ -227,6 +227,12 @@ def extras(torch, steps, dev):
                               "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 3),
                               "total_us": round(us_s + us_k, 2),
                               "total_hbm_frac": round((b_s + M * L * 4 + M * k * 4) / (us_s + us_k) / 1e3 / HBM_PEAK_GBS, 3)}
+    # the same scores over the KI page layout (64-key pages of 8448 B), 20 rotating page sets
+    pages = [si.ki_pages_from_flat(kc, ksc) for kc, ksc in caches]
+    del caches
+    us_p = _graph_time_us(torch, lambda i: si.sparse_index_paged(q, qsc, pages[i % 20], w, logits, L - 4, L), st, 5)
+    out["indexer_paged_128k_M4"] = {"scores_us": round(us_p, 2), "scores_GBs": round(b_s / us_p / 1e3, 1),
+                                    "scores_hbm_frac": round(b_s / us_p / 1e3 / HBM_PEAK_GBS, 3)}
     return out
 
 

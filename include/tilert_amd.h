@@ -23,6 +23,8 @@
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
  *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
+ *   tl_indexer_fp8_scores_paged  the same over KI pages    pd_vllm/profiles/mla_nsa.py:211-228
+ *   tl_ki_cache_write      writer of the KI page format    pd_vllm/profiles/mla_nsa.py:17-41
  *   tl_topk_rows           topk_accurate_op               .../ops/topk.py:62-109
  *   (sparse_index_topk_dsv32_op, .../ops/sparse_index.py:72-128, = scores + top-k)
  */
@@ -143,6 +145,26 @@ int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
                           const void* k_fp8, const float* k_s, const void* w_bf16,
                           float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
                           int64_t cur_pos, void* stream);
+
+/* Paged variant: the key cache in pd_vllm's KI page layout
+ * (pd_vllm/profiles/mla_nsa.py:17-41,211-228): ki_pages u8 [n_pages, 8448], page p =
+ * 64 keys x 128 fp8 (8192 B) followed by their 64 fp32 scales (256 B); key l lives in
+ * page l / 64, row l % 64.  L <= 64 * n_pages; pages 16-byte aligned.  Bit-identical to
+ * tl_indexer_fp8_scores on the equivalent flat cache.  Replaces sparse_index_op's cache
+ * read (ops/sparse_index.py:11-69) for the cache format MlaNsaProfile._dequant_ki reads. */
+int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per_head,
+                                const void* ki_pages, int64_t n_pages, const void* w_bf16,
+                                float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
+                                int64_t cur_pos, void* stream);
+
+/* Write `rows` keys (bf16 [rows, 128]) into KI pages at positions pos .. pos+rows-1:
+ * per key s = the act_quant group scale of its amax (scale_mode as tl_act_quant), fp8 =
+ * e4m3fn(clamp(k / s, +-448)), stored at page (pos+i) / 64, row (pos+i) % 64, its scale
+ * after the page's fp8 block.  The producer side of the format MlaNsaProfile._dequant_ki
+ * reads (mla_nsa.py:211-228); the key rotation of layernorm_rope_rotate
+ * (ops/layernorm_rope_rotate.py:206-220) happens upstream.  pos + rows <= 64 * n_pages. */
+int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t n_pages, int64_t pos,
+                      int scale_mode, void* stream);
 
 /* Exact per-row top-k.  logits fp32 [rows, ld]; row i considers columns
  * [0, valid_base + 1 + i) (clamped to [0, ld]) -- topk_accurate's convention with

@@ -158,3 +158,69 @@ def test_sparse_index_topk_128k(cuda):
     want = ref.indexer_scores(q, qs, kk, ks, w, L - 4)
     _scores_close(logits, want)
     _assert_topk_set(idx, want, [L - 3, L - 2, L - 1, L], k)
+
+
+@pytest.mark.parametrize("M,H,L,cur_pos,per_head", [
+    (4, 64, 5000, 4996, False),    # last page and last tile partial
+    (4, 64, 1000, 500, True),      # masked tail, per-head q scales
+    (8, 32, 640, 639, False),      # whole pages only
+    (4, 64, 131072, 131068, False),
+])
+def test_paged_indexer_matches_flat(cuda, M, H, L, cur_pos, per_head):
+    """The KI page layout (mla_nsa.py:17-41,211-228) read directly gives bit-identical
+    logits to the flat cache holding the same fp8 keys and scales."""
+    g = synth.gen(M * 7 + L)
+    q, qs, k, ks, w = synth.indexer_inputs(M, H, L, g)
+    if per_head:
+        qs = (torch.rand(M, H, generator=g) + 0.5) * qs[:, None]
+    q, qs, k, ks, w = (t.to(cuda).contiguous() for t in (q, qs, k, ks, w))
+    pages = si.ki_pages_from_flat(k, ks)
+    flat = torch.full((M, L + 8), 7.0, device=cuda)
+    paged = torch.full((M, L + 8), 7.0, device=cuda)
+    si.sparse_index(q, qs, k, ks, w, flat, cur_pos)
+    si.sparse_index_paged(q, qs, pages, w, paged, cur_pos, L)
+    assert torch.equal(flat, paged)
+    if L <= 5000:
+        _scores_close(paged[:, :L], ref.indexer_scores(q.cpu(), qs.cpu(), k.cpu(), ks.cpu(), w.cpu(), cur_pos))
+
+
+@pytest.mark.parametrize("scale_fmt", ["div", None, "ue8m0"])
+def test_ki_cache_write_matches_act_quant(cuda, scale_fmt):
+    """Keys written into the pages equal act_quant's bytes and scales for the same rows,
+    at positions that straddle page boundaries; other rows stay untouched."""
+    from tilert_amd import kernel as K
+    g = synth.gen(5)
+    n, pos, n_pages = 200, 61, 6
+    keys = torch.randn(n, 128, generator=g)
+    keys[3] = 0.0                      # all-zero key: the amax floor
+    keys[7] *= 1e4                     # large values
+    keys = keys.to(torch.bfloat16).to(cuda)
+    pages = torch.zeros(n_pages, si.KI_PAGE_BYTES, dtype=torch.uint8, device=cuda)
+    si.ki_cache_write(keys, pages, pos, scale_fmt=scale_fmt)
+    y, s = K.act_quant(keys, scale_fmt=scale_fmt)
+    full_k = torch.zeros(n_pages * 64, 128, dtype=torch.float8_e4m3fn, device=cuda)
+    full_s = torch.zeros(n_pages * 64, dtype=torch.float32, device=cuda)
+    full_k[pos:pos + n] = y
+    full_s[pos:pos + n] = s.reshape(-1)
+    assert torch.equal(pages, si.ki_pages_from_flat(full_k, full_s))
+
+
+def test_ki_write_then_paged_scores(cuda):
+    """Writer and paged reader together: keys written at the decode positions score like
+    the flat cache built from the same quantisation."""
+    g = synth.gen(11)
+    M, H, L = 4, 64, 3000
+    q, qs, _, _, w = synth.indexer_inputs(M, H, L, g)
+    keys = torch.randn(L, 128, generator=g).to(torch.bfloat16)
+    q, qs, w, keys = (t.to(cuda).contiguous() for t in (q, qs, w, keys))
+    pages = torch.zeros((L + 63) // 64, si.KI_PAGE_BYTES, dtype=torch.uint8, device=cuda)
+    si.ki_cache_write(keys[:2000], pages, 0)          # prefill
+    for p0 in range(2000, L, 250):                    # then decode steps
+        si.ki_cache_write(keys[p0:p0 + 250].contiguous(), pages, p0)
+    from tilert_amd import kernel as K
+    kq, ks = K.act_quant(keys, scale_fmt="div")
+    flat = torch.empty(M, L, device=cuda)
+    paged = torch.empty(M, L, device=cuda)
+    si.sparse_index(q, qs, kq, ks.reshape(-1).contiguous(), w, flat, L - 4)
+    si.sparse_index_paged(q, qs, pages, w, paged, L - 4, L)
+    assert torch.equal(flat, paged)

@@ -40,6 +40,10 @@ SIGNATURES: dict[str, tuple] = {
     "tl_indexer_fp8_scores": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _c_void_p,
                                      _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                      _c_void_p]),
+    "tl_indexer_fp8_scores_paged": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _i64,
+                                           _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
+                                           _c_void_p]),
+    "tl_ki_cache_write": (_int, [_c_void_p, _i64, _c_void_p, _i64, _i64, _int, _c_void_p]),
     "tl_topk_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "tl_topk_rows": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _size,
                             _c_void_p]),

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/tilert_amd.h"
+
 namespace tl {
 
 constexpr int kBlock = 128;
@@ -59,6 +61,20 @@ __device__ inline uint32_t f32_to_e4m3(float v) {
     if (code > 0x7eu) code = 0x7eu;  // only reachable for |v| > 448 (clamped by callers)
   }
   return code | sign;
+}
+
+// Quantisation scale of a 128-element group from its fp32 amax; mirrors
+// refs/kernel.py:186-191 (amax floor 1e-4, s = amax * fp32(1/448)) and the power-of-two
+// round-scale form :140-151; TL_SCALE_DIV is BASELINE's amax / 448.
+__device__ inline float group_scale(float amax, int scale_mode) {
+  amax = fmaxf(amax, 1e-4f);
+  if (scale_mode == TL_SCALE_UE8M0) {
+    uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
+    int e = static_cast<int>((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0 ? 1 : 0);
+    return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+  }
+  if (scale_mode == TL_SCALE_DIV) return amax / 448.0f;
+  return amax * (1.0f / 448.0f);
 }
 
 // --------------------------------------------------------------- MFMA tile helper

@@ -64,7 +64,19 @@ struct IdxShape {
   static_assert(kIdxWaves % SPLIT == 0 && TW <= 4 && QT * 16 <= THREADS, "work split");
 };
 
-template <int M, int H, int TW, int TPW>
+// Key cache layouts.  Flat: fp8 [L, 128] plus fp32 scales [L].  Paged (PAGED): the
+// 64-token pages of pd_vllm/profiles/mla_nsa.py:38-41,211-228 -- page p is 64 x 128 fp8
+// (8192 B) followed by the 64 tokens' fp32 scales (256 B), 8448 B in all; key l sits in
+// page l / 64, row l % 64.  A 16-key tile is still 2 KB contiguous either way.
+constexpr int kKiPageKeys = 64;
+constexpr int kKiPageBytes = kKiPageKeys * 128 + kKiPageKeys * 4;  // 8448
+
+template <bool PAGED>
+__device__ inline int64_t key_tile_byte(int tile) {
+  return PAGED ? static_cast<int64_t>(tile >> 2) * kKiPageBytes + (tile & 3) * 2048 : static_cast<int64_t>(tile) * 2048;
+}
+
+template <int M, int H, int TW, int TPW, bool PAGED>
 __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ q_s, int q_s_per_head,
     const uint8_t* __restrict__ k, const float* __restrict__ k_s, const uint16_t* __restrict__ w,
@@ -96,15 +108,18 @@ __global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
   for (int u = 0; u < S::KSPT; ++u) {
     const int e = tid + u * S::THREADS;  // key e % 16 of workgroup tile e / 16
     const int key = min(min(wg_tile + e / 16, n_tiles - 1) * 16 + (e & 15), L - 1);
-    ksv[u] = k_s[key];
+    ksv[u] = PAGED ? *reinterpret_cast<const float*>(k + static_cast<int64_t>(key / kKiPageKeys) * kKiPageBytes +
+                                                     kKiPageKeys * 128 + (key % kKiPageKeys) * 4)
+                   : k_s[key];
   }
   // key chunk c of phase p: phase tile pt = c / 128 (range pt / TPP, its tile
   // p * TPP + pt % TPP), row (c / 8) % 16, 16-byte chunk c % 8 -- contiguous 1 KB reads
   auto key_src = [&](int p, int c) {
     const int pt = min(c >> 7, S::PT - 1);
     const int tile = min(wg_tile + (pt / S::TPP) * TPW + p * S::TPP + pt % S::TPP, n_tiles - 1);
-    const int64_t byte = static_cast<int64_t>(tile) * 2048 + (c & 127) * 16;
-    return reinterpret_cast<const u32x4v*>(k + min(byte, static_cast<int64_t>(L) * kBlock - 16));
+    const int64_t byte = key_tile_byte<PAGED>(tile) + (c & 127) * 16;
+    // flat: a short last tile stops at the cache end; paged: pages are whole
+    return reinterpret_cast<const u32x4v*>(k + (PAGED ? byte : min(byte, static_cast<int64_t>(L) * kBlock - 16)));
   };
   u32x4v kv[S::PH][S::KPT];
 #pragma unroll
@@ -216,18 +231,18 @@ __global__ void fill_masked_kernel(float* __restrict__ logits, int M, int64_t ld
 
 constexpr int kIdxMaxWaves = 4096;  // 16 per CU: beyond that a wave takes more key tiles
 
-template <int M, int H, int TW, int TPW>
+template <int M, int H, int TW, int TPW, bool PAGED>
 static int launch_indexer_t(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
                             const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
                             int L, int64_t ld, int64_t cur_pos, int n_tiles) {
   using S = IdxShape<M, H, TW, TPW>;
-  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, TW, TPW>);
+  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, TW, TPW, PAGED>);
   if (S::LDS > 64 * 1024) {
     const int rc = allow_dynamic_lds(fn, S::LDS, "indexer");
     if (rc) return rc;
   }
   const dim3 grid(static_cast<unsigned>(cdiv(n_tiles, static_cast<int64_t>(S::NT))));
-  hipLaunchKernelGGL((indexer_kernel<M, H, TW, TPW>), grid, dim3(kIdxWaves * 64), S::LDS, st, q, q_s, per_head, k,
+  hipLaunchKernelGGL((indexer_kernel<M, H, TW, TPW, PAGED>), grid, dim3(kIdxWaves * 64), S::LDS, st, q, q_s, per_head, k,
                      k_s, w, logits, L, ld, cur_pos, n_tiles);
   return check_launch("indexer");
 }
@@ -241,7 +256,7 @@ constexpr int pick_tw(int M, int TPT) {
   return tw;
 }
 
-template <int M, int H>
+template <int M, int H, bool PAGED>
 static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
                           const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
                           int L, int64_t ld, int64_t cur_pos, int n_tiles) {
@@ -252,27 +267,23 @@ static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, in
   int tpw = 1;
   while (tpw < 8 && static_cast<int64_t>(n_tiles) * SPLIT > static_cast<int64_t>(kIdxMaxWaves) * tpw) tpw *= 2;
   switch (tpw) {
-    case 1: return launch_indexer_t<M, H, TW, 1>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    case 2: return launch_indexer_t<M, H, TW, 2>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    case 4: return launch_indexer_t<M, H, TW, 4>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    default: return launch_indexer_t<M, H, TW, 8>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 1: return launch_indexer_t<M, H, TW, 1, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 2: return launch_indexer_t<M, H, TW, 2, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 4: return launch_indexer_t<M, H, TW, 4, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    default: return launch_indexer_t<M, H, TW, 8, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
   }
 }
 
-}  // namespace tl
-
-using namespace tl;
-
-extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
-                                     const void* k_fp8, const float* k_s, const void* w_bf16,
-                                     float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
-                                     int64_t cur_pos, void* stream) {
-  if (H != 32 && H != 64) { set_error("indexer: H=%lld must be 32 or 64", (long long)H); return kErrUnsupported; }
-  if (M < 1 || M * H > 256) { set_error("indexer: need 1 <= M and M*H <= 256 (M=%lld H=%lld)", (long long)M, (long long)H); return kErrUnsupported; }
-  if (L < 0 || L > (1ll << 30) || ld < L) { set_error("indexer: bad L=%lld / ld=%lld", (long long)L, (long long)ld); return kErrArg; }
-  if (cur_pos < 0) { set_error("indexer: cur_pos=%lld must be >= 0", (long long)cur_pos); return kErrArg; }
-  if (!q_fp8 || !q_s || !k_fp8 || !k_s || !w_bf16 || !logits) { set_error("indexer: null pointer"); return kErrArg; }
-  if ((reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(k_fp8)) & 15) { set_error("indexer: q and k must be 16-byte aligned"); return kErrArg; }
+template <bool PAGED>
+static int indexer_scores(const char* who, const void* q_fp8, const float* q_s, int q_s_per_head, const void* k_fp8,
+                          const float* k_s, const void* w_bf16, float* logits, int64_t M, int64_t H, int64_t L,
+                          int64_t ld, int64_t cur_pos, void* stream) {
+  if (H != 32 && H != 64) { set_error("%s: H=%lld must be 32 or 64", who, (long long)H); return kErrUnsupported; }
+  if (M < 1 || M * H > 256) { set_error("%s: need 1 <= M and M*H <= 256 (M=%lld H=%lld)", who, (long long)M, (long long)H); return kErrUnsupported; }
+  if (L < 0 || L > (1ll << 30) || ld < L) { set_error("%s: bad L=%lld / ld=%lld", who, (long long)L, (long long)ld); return kErrArg; }
+  if (cur_pos < 0) { set_error("%s: cur_pos=%lld must be >= 0", who, (long long)cur_pos); return kErrArg; }
+  if (!q_fp8 || !q_s || !k_fp8 || (!PAGED && !k_s) || !w_bf16 || !logits) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(k_fp8)) & 15) { set_error("%s: q and k must be 16-byte aligned", who); return kErrArg; }
   if (L == 0) return kOk;
   hipStream_t st = (hipStream_t)stream;
   // keys past the last token's position are masked for every token: no need to read them
@@ -287,10 +298,84 @@ extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_
   const uint16_t* w = (const uint16_t*)w_bf16;
   const int Li = static_cast<int>(L);
 #define TL_IDX(MM, HH) \
-  if (M == MM && H == HH) return launch_indexer<MM, HH>(st, q, q_s, q_s_per_head, k, k_s, w, logits, Li, ld, cur_pos, n_tiles);
+  if (M == MM && H == HH) return launch_indexer<MM, HH, PAGED>(st, q, q_s, q_s_per_head, k, k_s, w, logits, Li, ld, cur_pos, n_tiles);
   TL_IDX(1, 64) TL_IDX(2, 64) TL_IDX(3, 64) TL_IDX(4, 64)
   TL_IDX(1, 32) TL_IDX(2, 32) TL_IDX(3, 32) TL_IDX(4, 32) TL_IDX(5, 32) TL_IDX(6, 32) TL_IDX(7, 32) TL_IDX(8, 32)
 #undef TL_IDX
-  set_error("indexer: unsupported M=%lld H=%lld", (long long)M, (long long)H);
+  set_error("%s: unsupported M=%lld H=%lld", who, (long long)M, (long long)H);
   return kErrUnsupported;
+}
+
+// One thread per 8 key elements, 16 threads per key: quantise the key like act_quant
+// (amax, scale by scale_mode, e4m3fn of the clamped quotient) and write it into its page.
+__global__ __launch_bounds__(256) void ki_write_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ pages,
+                                                       int64_t rows, int64_t pos, int scale_mode) {
+  const int64_t tid = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t row = tid >> 4;
+  const bool live = row < rows;
+  uint4 raw = make_uint4(0, 0, 0, 0);
+  if (live) raw = reinterpret_cast<const uint4*>(x)[tid];
+  float v[8];
+  v[0] = bf16_to_f32(raw.x & 0xffff); v[1] = bf16_to_f32(raw.x >> 16);
+  v[2] = bf16_to_f32(raw.y & 0xffff); v[3] = bf16_to_f32(raw.y >> 16);
+  v[4] = bf16_to_f32(raw.z & 0xffff); v[5] = bf16_to_f32(raw.z >> 16);
+  v[6] = bf16_to_f32(raw.w & 0xffff); v[7] = bf16_to_f32(raw.w >> 16);
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  const float sc = group_scale(amax, scale_mode);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo |= f32_to_e4m3(fminf(fmaxf(v[i] / sc, -kE4m3Max), kE4m3Max)) << (8 * i);
+    hi |= f32_to_e4m3(fminf(fmaxf(v[i + 4] / sc, -kE4m3Max), kE4m3Max)) << (8 * i);
+  }
+  if (live) {
+    const int64_t key = pos + row;
+    uint8_t* page = pages + (key / kKiPageKeys) * kKiPageBytes;
+    const int r = static_cast<int>(key % kKiPageKeys);
+    *reinterpret_cast<uint2*>(page + r * 128 + (tid & 15) * 8) = make_uint2(lo, hi);
+    if ((tid & 15) == 0) *reinterpret_cast<float*>(page + kKiPageKeys * 128 + r * 4) = sc;
+  }
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_s_per_head,
+                                     const void* k_fp8, const float* k_s, const void* w_bf16,
+                                     float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
+                                     int64_t cur_pos, void* stream) {
+  return indexer_scores<false>("indexer", q_fp8, q_s, q_s_per_head, k_fp8, k_s, w_bf16, logits, M, H, L, ld, cur_pos,
+                               stream);
+}
+
+extern "C" int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per_head,
+                                           const void* ki_pages, int64_t n_pages, const void* w_bf16,
+                                           float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
+                                           int64_t cur_pos, void* stream) {
+  if (n_pages < 0 || L > n_pages * kKiPageKeys) {
+    set_error("indexer_paged: L=%lld keys need %lld pages (got %lld)", (long long)L, (long long)cdiv(L, kKiPageKeys), (long long)n_pages);
+    return kErrArg;
+  }
+  return indexer_scores<true>("indexer_paged", q_fp8, q_s, q_s_per_head, ki_pages, nullptr, w_bf16, logits, M, H, L, ld,
+                              cur_pos, stream);
+}
+
+extern "C" int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t n_pages, int64_t pos,
+                                 int scale_mode, void* stream) {
+  if (rows < 0 || pos < 0 || pos + rows > n_pages * kKiPageKeys) {
+    set_error("ki_cache_write: keys [%lld, %lld) exceed %lld pages", (long long)pos, (long long)(pos + rows), (long long)n_pages);
+    return kErrArg;
+  }
+  if (scale_mode < 0 || scale_mode > 2) { set_error("ki_cache_write: bad scale_mode %d", scale_mode); return kErrArg; }
+  if (!k_bf16 || !ki_pages) { set_error("ki_cache_write: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(k_bf16) | reinterpret_cast<uintptr_t>(ki_pages)) & 15) { set_error("ki_cache_write: pointers must be 16-byte aligned"); return kErrArg; }
+  if (rows == 0) return kOk;
+  hipLaunchKernelGGL(ki_write_kernel, dim3(cdiv(rows * 16, 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)k_bf16, (uint8_t*)ki_pages, rows, pos, scale_mode);
+  return check_launch("ki_cache_write");
 }

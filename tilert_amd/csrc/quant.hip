@@ -5,18 +5,6 @@
 
 namespace tl {
 
-// Group scale from the fp32 amax; mirrors refs/kernel.py:186-191 and :140-151.
-__device__ inline float group_scale(float amax, int scale_mode) {
-  amax = fmaxf(amax, 1e-4f);
-  if (scale_mode == TL_SCALE_UE8M0) {
-    uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
-    int e = static_cast<int>((bits >> 23) & 0xffu) - 127 + ((bits & 0x7fffffu) != 0 ? 1 : 0);
-    return __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
-  }
-  if (scale_mode == TL_SCALE_DIV) return amax / 448.0f;
-  return amax * (1.0f / 448.0f);
-}
-
 // One thread = 8 consecutive elements; 16 threads = one 128-element group.
 __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restrict__ x,
                                                         uint8_t* __restrict__ y,

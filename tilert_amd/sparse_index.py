@@ -12,8 +12,12 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .kernel import _require_cuda, _stream
+from .kernel import SCALE_MODES, _require_cuda, _stream
 from .topk import topk_rows
+
+# The KI page format of pd_vllm/profiles/mla_nsa.py:17-41 (PAGE_SIZE, KI_PAGE_BYTES).
+KI_PAGE_KEYS = 64
+KI_PAGE_BYTES = KI_PAGE_KEYS * 128 + KI_PAGE_KEYS * 4  # 8448
 
 
 def _check(q, q_scale, kv, k_scale, weights, logits, heads=(32, 64)):
@@ -88,3 +92,70 @@ def sparse_index_topk(q: torch.Tensor, q_scale: torch.Tensor, kv: torch.Tensor,
         raise ValueError("indices must be an int32 [M, k] tensor")
     k = indices.numel() // M
     topk_rows(logits.reshape(M, -1), valid_base=int(cur_pos), k=k, out=indices.reshape(M, k))
+
+
+def ki_pages_from_flat(kv: torch.Tensor, k_scale: torch.Tensor) -> torch.Tensor:
+    """The KI page image of a flat fp8 cache: kv e4m3fn [L, 128] and k_scale fp32 [L] ->
+    uint8 [ceil(L/64), 8448]; page p holds keys 64p .. 64p+63 (fp8 rows, then their
+    scales), the layout ``MlaNsaProfile._dequant_ki`` reads (mla_nsa.py:211-228).  Rows
+    past L are zero.  A layout conversion in torch (load time), not a hot-path op."""
+    if kv.dtype != torch.float8_e4m3fn or kv.dim() != 2 or kv.shape[1] != 128:
+        raise ValueError("kv must be a float8_e4m3fn [L, 128] tensor")
+    if k_scale.dtype != torch.float32 or k_scale.numel() != kv.shape[0]:
+        raise ValueError("k_scale must be a float32 [L] tensor")
+    L = kv.shape[0]
+    n_pages = (L + KI_PAGE_KEYS - 1) // KI_PAGE_KEYS
+    pages = torch.zeros(n_pages, KI_PAGE_BYTES, dtype=torch.uint8, device=kv.device)
+    full = torch.zeros(n_pages * KI_PAGE_KEYS, 128, dtype=torch.uint8, device=kv.device)
+    full[:L] = kv.view(torch.uint8)
+    sc = torch.zeros(n_pages * KI_PAGE_KEYS, dtype=torch.float32, device=kv.device)
+    sc[:L] = k_scale.reshape(-1)
+    pages[:, :KI_PAGE_KEYS * 128] = full.reshape(n_pages, KI_PAGE_KEYS * 128)
+    pages[:, KI_PAGE_KEYS * 128:] = sc.reshape(n_pages, KI_PAGE_KEYS).view(torch.uint8).reshape(n_pages, -1)
+    return pages
+
+
+def ki_cache_write(keys: torch.Tensor, ki_pages: torch.Tensor, pos: int, scale_fmt: str | None = "div") -> None:
+    """Quantise ``keys`` (bf16 [n, 128]) per key to e4m3fn with an fp32 scale and store them
+    at positions pos .. pos+n-1 of ``ki_pages`` (uint8 [n_pages, 8448]).  ``scale_fmt`` as in
+    ``act_quant``; the default "div" is BASELINE's per-token amax / 448."""
+    if keys.dtype != torch.bfloat16 or keys.dim() != 2 or keys.shape[1] != 128 or not keys.is_contiguous():
+        raise ValueError("keys must be a contiguous bfloat16 [n, 128] tensor")
+    if ki_pages.dtype != torch.uint8 or ki_pages.dim() != 2 or ki_pages.shape[1] != KI_PAGE_BYTES \
+            or not ki_pages.is_contiguous():
+        raise ValueError(f"ki_pages must be a contiguous uint8 [n_pages, {KI_PAGE_BYTES}] tensor")
+    if keys.device != ki_pages.device:
+        raise ValueError("keys and ki_pages must be on the same device")
+    _require_cuda("ki_cache_write", keys)
+    _lib.call("tl_ki_cache_write", keys.data_ptr(), keys.shape[0], ki_pages.data_ptr(), ki_pages.shape[0],
+              int(pos), SCALE_MODES.get(scale_fmt, 1), _stream(keys))
+
+
+def sparse_index_paged(q: torch.Tensor, q_scale: torch.Tensor, ki_pages: torch.Tensor,
+                       weights: torch.Tensor, logits: torch.Tensor, cur_pos: int, seq_len: int) -> None:
+    """``sparse_index`` over the paged KI cache (uint8 [n_pages, 8448], keys 0 .. seq_len-1):
+    bit-identical to ``sparse_index`` on the equivalent flat cache."""
+    if ki_pages.dtype != torch.uint8 or ki_pages.dim() != 2 or ki_pages.shape[1] != KI_PAGE_BYTES \
+            or not ki_pages.is_contiguous():
+        raise ValueError(f"ki_pages must be a contiguous uint8 [n_pages, {KI_PAGE_BYTES}] tensor")
+    L = int(seq_len)
+    if L < 0 or L > ki_pages.shape[0] * KI_PAGE_KEYS:
+        raise ValueError("seq_len exceeds the pages' capacity")
+    # validate q / weights / logits exactly as the flat op does (a [L, 128] view stands in
+    # for the cache in the shape checks)
+    _check(q, q_scale, torch.empty(0, 128, dtype=torch.float8_e4m3fn, device=q.device),
+           torch.empty(0, dtype=torch.float32, device=q.device), weights, logits)
+    if ki_pages.device != q.device:
+        raise ValueError("sparse_index inputs must be on the same device")
+    H = q.shape[-2]
+    M = q.numel() // (H * 128)
+    if weights.numel() != M * H:
+        raise ValueError("weights must be [M, H]")
+    per_head = q_scale.numel() == M * H and H > 1
+    if not per_head and q_scale.numel() != M:
+        raise ValueError("q_scale must be [M] or [M, H]")
+    ld = logits.shape[-1]
+    if logits.numel() != M * ld or ld < L:
+        raise ValueError("logits must be [M, ld] with ld >= seq_len")
+    _lib.call("tl_indexer_fp8_scores_paged", q.data_ptr(), q_scale.data_ptr(), int(per_head), ki_pages.data_ptr(),
+              ki_pages.shape[0], weights.data_ptr(), logits.data_ptr(), M, H, L, ld, int(cur_pos), _stream(q))
