@@ -137,6 +137,19 @@ def extras(torch, steps, dev):
     out = {}
     st = max(10, steps // 10)
 
+    # the fused producer of the linears' input: RMSNorm + act_quant, M = 4 x 7168
+    from tilert_amd.rmsnorm import rmsnorm_quant
+    xs_ = [torch.randn(4, 7168, device=dev).to(torch.bfloat16) for _ in range(4)]
+    gam = torch.ones(7168, device=dev)
+    yb = torch.empty(4, 7168, dtype=torch.bfloat16, device=dev)
+    yq = torch.empty(4, 7168, dtype=torch.float8_e4m3fn, device=dev)
+    ysc = torch.empty(4, 56, dtype=torch.float32, device=dev)
+    logs = torch.zeros(1, device=dev)
+    us = _graph_time_us(torch, lambda i: rmsnorm_quant(xs_[i % 4], gam, yb, yq, ysc, logs, model_arch="deepseek_v3_2"),
+                        st, 5)
+    b = 4 * 7168 * 2 + 7168 * 4 + 4 * 7168 * 2 + 4 * 7168 + 4 * 56 * 4
+    out["rmsnorm_quant_M4"] = {"us": round(us, 2), "bytes": b}
+
     # config 1: MLA projections at the TP=8 share, M = 4
     mla = {"wq_a": (7168, 1536), "wq_b": (1536, 3072), "wkv_a": (7168, 576), "wkv_b": (512, 4096), "wo": (2048, 7168)}
     tot_us, tot_b = 0.0, 0

@@ -22,6 +22,7 @@
  *   tl_fp8_pack_weight  the per-op weight converters (load-time layout change)
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
+ *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
  *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
  *   tl_indexer_fp8_scores_paged  the same over KI pages    pd_vllm/profiles/mla_nsa.py:211-228
  *   tl_ki_cache_write      writer of the KI page format    pd_vllm/profiles/mla_nsa.py:17-41
@@ -134,6 +135,16 @@ int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, const float* 
                         const int32_t* topk_idx, const float* topk_w, int64_t M, int64_t topk,
                         int64_t expert_begin, int64_t n_local, int64_t D, int64_t I,
                         void* y_bf16, void* stream);
+
+/* RMSNorm with optional activation quantisation (rmsnorm_quant_op / rmsnorm_op,
+ * ops/rmsnorm_quant.py:19-63; norm of tilert/models/common.py:92-133 without residual).
+ * x bf16 [rows, dim], gamma fp32 [dim]: y_bf16 = bf16(gamma * x * 1/sqrt(mean(x^2) + eps))
+ * (fp32 math); when y_fp8 / y_scale are non-null, they receive act_quant of y_bf16 per
+ * 1x128 group (fp8 e4m3fn [rows, dim], fp32 [rows, dim/128], scale_mode as
+ * tl_act_quant) -- bit-identical to tl_act_quant applied to y_bf16.  dim % 128 == 0,
+ * dim <= 16384; pointers 16-byte aligned. */
+int tl_rmsnorm_quant(const void* x_bf16, const float* gamma, float eps, int64_t rows, int64_t dim,
+                     void* y_bf16, void* y_fp8, float* y_scale, int scale_mode, void* stream);
 
 /* DSA lightning-indexer scores over an fp8 key cache.
  * q fp8 [M, H, 128]; q_s fp32 per token [M] (q_s_per_head = 0) or per (token, head)

@@ -66,6 +66,24 @@ def act_quant(
     return y.reshape(x.shape), s.reshape(*x.shape[:-1], K // block_size)
 
 
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``RMSNorm.forward`` without residual (tilert/models/common.py:110-128): fp32 math,
+    x * rsqrt(mean(x^2) + eps), times the fp32 weight, cast to bf16."""
+    xf = x.float()
+    var = xf.pow(2).mean(-1, keepdim=True)
+    xf = xf * torch.rsqrt(var + eps)
+    return (weight.float() * xf).to(torch.bfloat16)
+
+
+def rmsnorm_quant(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                  scale_mode: int = SCALE_MODE_REFERENCE):
+    """``rmsnorm_quant_op`` (ops/rmsnorm_quant.py:19-63): the bf16 norm, then act_quant of
+    those bf16 values per 1x128 group."""
+    y = rmsnorm(x, weight, eps)
+    q, s = act_quant(y, BLOCK, scale_mode)
+    return y, q, s
+
+
 def act_dequant(y: torch.Tensor, s: torch.Tensor, block_size: int = BLOCK) -> torch.Tensor:
     """fp32 x = fp8 * group scale, as the goldens do (projx_wqkva.py:280-285)."""
     K = y.shape[-1]

@@ -158,3 +158,48 @@ def test_topk_vs_selection_brute_force_with_ties():
     got = ref.topk_rows(x, valid, 32)
     assert np.array_equal(got.numpy().astype(np.int64), want)
     assert torch.all(got[2, 10:] == -1)
+
+
+# --------------------------------------------------------------------------- rmsnorm
+def _bf16_ulp(v: torch.Tensor) -> torch.Tensor:
+    e = torch.floor(torch.log2(v.abs().clamp_min(1e-30)))
+    return torch.pow(2.0, e - 7)
+
+
+def test_rmsnorm_vs_fp64_and_one_hot_divisor():
+    g = synth.gen(21)
+    x = (torch.randn(6, 7168, generator=g) * 3).to(torch.bfloat16)
+    w = 1 + 0.1 * torch.randn(7168, generator=g)
+    out = ref.rmsnorm(x, w).double()
+    xd = x.double()
+    want = w.double() * xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    assert torch.all((out - want).abs() <= _bf16_ulp(want))  # within one bf16 step of fp64
+    # one-hot row: mean(x^2) = a^2 / dim, so out_i = w_i * a / sqrt(a^2/dim + eps) ~ w_i * sqrt(dim)
+    oh = torch.zeros(1, 7168, dtype=torch.bfloat16)
+    oh[0, 5] = 2.0
+    o = ref.rmsnorm(oh, w).double()[0]
+    exp = w[5].double() * 2.0 / math.sqrt(4.0 / 7168 + 1e-6)
+    assert abs(o[5].item() - exp) <= _bf16_ulp(torch.tensor(exp)).item()
+    assert torch.all(o[torch.arange(7168) != 5] == 0)
+
+
+def test_rmsnorm_power_of_two_invariance_and_constant_rows():
+    g = synth.gen(22)
+    x = torch.randn(3, 1024, generator=g).to(torch.bfloat16)
+    w = torch.rand(1024, generator=g) + 0.5
+    # with eps = 0, scaling x by 2^k scales mean(x^2) by 4^k exactly and rsqrt by 2^-k
+    assert torch.equal(ref.rmsnorm(x, w, eps=0.0), ref.rmsnorm(x * 8, w, eps=0.0))
+    # a constant row c normalises to w * c / sqrt(c^2 + eps)
+    c = torch.full((1, 1024), -0.75, dtype=torch.bfloat16)
+    o = ref.rmsnorm(c, w).double()[0]
+    want = w.double() * -0.75 / math.sqrt(0.5625 + 1e-6)
+    assert torch.all((o - want).abs() <= _bf16_ulp(want))
+
+
+def test_rmsnorm_quant_is_act_quant_of_the_bf16_norm():
+    g = synth.gen(23)
+    x = torch.randn(4, 512, generator=g).to(torch.bfloat16)
+    w = torch.ones(512)
+    y, q, s = ref.rmsnorm_quant(x, w)
+    q2, s2 = ref.act_quant(y)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)

@@ -103,9 +103,118 @@ __global__ __launch_bounds__(256) void weight_dequant_kernel(const uint8_t* __re
   else static_cast<float*>(out)[i] = v;
 }
 
+// RMSNorm (tilert/models/common.py:92-133, no residual): y = bf16(gamma * x * rsqrt(mean(x^2)
+// + eps)) in fp32, then -- when y8/ys are given -- act_quant of those bf16 values per
+// 1x128 group (rmsnorm_quant_op, ops/rmsnorm_quant.py:19-63).  One 1024-thread workgroup
+// per row; thread t takes the 8-element chunks t and t+1024, so 16 consecutive threads
+// hold one 128-element group.  Every load (x and gamma) is issued up front: the row costs
+// one memory round trip.  rsqrt is 1 / sqrt with IEEE sqrt and division, as torch's.
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxChunks = 2;  // dim <= 2 * 1024 * 8 = 16384
+
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ gamma, float eps, int dim,
+    uint16_t* __restrict__ y, uint8_t* __restrict__ y8, float* __restrict__ ys, int scale_mode) {
+  __shared__ float part[kNormThreads / 64];
+  const int row = blockIdx.x;
+  const int nch = dim / 8;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * dim);
+  uint4 raw[kNormMaxChunks];
+  float4 g0[kNormMaxChunks], g1[kNormMaxChunks];
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {  // clamped, unconditional loads
+    const int c = min(static_cast<int>(threadIdx.x) + i * kNormThreads, nch - 1);
+    raw[i] = xr[c];
+    g0[i] = reinterpret_cast<const float4*>(gamma)[2 * c];
+    g1[i] = reinterpret_cast<const float4*>(gamma)[2 * c + 1];
+  }
+  float v[kNormMaxChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    const bool live = static_cast<int>(threadIdx.x) + i * kNormThreads < nch;
+    const uint32_t w4[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i][2 * j] = live ? bf16_to_f32(w4[j] & 0xffff) : 0.f;
+      v[i][2 * j + 1] = live ? bf16_to_f32(w4[j] >> 16) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(v[i][j], v[i][j], ss);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / 64; ++w) tot += part[w];
+  const float r = 1.0f / __builtin_sqrtf(tot / static_cast<float>(dim) + eps);
+#pragma unroll
+  for (int i = 0; i < kNormMaxChunks; ++i) {
+    if (i * kNormThreads >= nch) break;  // workgroup-uniform
+    const int c = static_cast<int>(threadIdx.x) + i * kNormThreads;
+    const bool live = c < nch;
+    const float gv[8] = {g0[i].x, g0[i].y, g0[i].z, g0[i].w, g1[i].x, g1[i].y, g1[i].z, g1[i].w};
+    uint16_t b[8];
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      b[j] = f32_to_bf16(gv[j] * (v[i][j] * r));
+      q[j] = bf16_to_f32(b[j]);
+    }
+    if (live)
+      reinterpret_cast<uint4*>(y + static_cast<int64_t>(row) * dim)[c] =
+          make_uint4(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16),
+                     b[4] | (static_cast<uint32_t>(b[5]) << 16), b[6] | (static_cast<uint32_t>(b[7]) << 16));
+    if (y8) {  // kernel-uniform
+      float amax = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(q[j]));
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+      const float sc = group_scale(amax, scale_mode);
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        lo |= f32_to_e4m3(fminf(fmaxf(q[j] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
+        hi |= f32_to_e4m3(fminf(fmaxf(q[j + 4] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
+      }
+      if (live) {
+        reinterpret_cast<uint2*>(y8 + static_cast<int64_t>(row) * dim)[c] = make_uint2(lo, hi);
+        if ((c & 15) == 0) ys[static_cast<int64_t>(row) * (dim / kBlock) + (c >> 4)] = sc;
+      }
+    }
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
+
+extern "C" int tl_rmsnorm_quant(const void* x_bf16, const float* gamma, float eps, int64_t rows, int64_t dim,
+                                void* y_bf16, void* y_fp8, float* y_scale, int scale_mode, void* stream) {
+  if (rows < 0 || dim <= 0 || dim % kBlock || dim > kNormMaxChunks * kNormThreads * 8) {
+    set_error("rmsnorm_quant: dim=%lld must be a positive multiple of 128, at most %d", (long long)dim,
+              kNormMaxChunks * kNormThreads * 8);
+    return kErrArg;
+  }
+  if (scale_mode < 0 || scale_mode > 2) { set_error("rmsnorm_quant: bad scale_mode %d", scale_mode); return kErrArg; }
+  if (!x_bf16 || !gamma || !y_bf16 || (!y_fp8) != (!y_scale)) {
+    set_error("rmsnorm_quant: null pointer (y_fp8 and y_scale are given together or not at all)");
+    return kErrArg;
+  }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(gamma) | reinterpret_cast<uintptr_t>(y_bf16) |
+       reinterpret_cast<uintptr_t>(y_fp8)) & 15) {
+    set_error("rmsnorm_quant: pointers must be 16-byte aligned");
+    return kErrArg;
+  }
+  if (rows == 0) return kOk;
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, gamma, eps, (int)dim, (uint16_t*)y_bf16,
+                     (uint8_t*)y_fp8, y_scale, scale_mode);
+  return check_launch("rmsnorm_quant");
+}
 
 extern "C" int tl_act_quant(const void* x_bf16, void* y_fp8, float* s, int64_t rows, int64_t K,
                             int64_t group, int scale_mode, void* stream) {
