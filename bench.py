@@ -160,9 +160,29 @@ def extras(torch, steps, dev):
         per[name] = {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)}
         tot_us += us
         tot_b += b
+    # the fused wq_a + wkv_a launch (projx_wqkva, the reference's own fusion of the two)
+    from tilert_amd.projx import pack_wqkva, projx_wqkva
+    pw = []
+    for c in range(8):
+        g = torch.Generator(device=dev).manual_seed(100 + c)
+        wq_, wqs_ = K_.weight_quant(torch.randn(1536, 7168, device=dev, generator=g) * 0.02)
+        wkv_, wkvs_ = K_.weight_quant(torch.randn(576, 7168, device=dev, generator=g) * 0.02)
+        pw.append(pack_wqkva(wq_, wqs_, wkv_, wkvs_, 512))
+    xq4, xs4 = K_.act_quant(torch.randn(1, 4, 7168, device=dev).to(torch.bfloat16))
+    q4 = torch.empty(1, 4, 1536, dtype=torch.bfloat16, device=dev)
+    kv4 = torch.empty(1, 4, 512, dtype=torch.bfloat16, device=dev)
+    pe4 = torch.empty(1, 128, 64, dtype=torch.bfloat16, device=dev)
+    cur4 = torch.tensor([7], dtype=torch.int32, device=dev)
+    us = _graph_time_us(torch, lambda i: projx_wqkva(xq4, xs4, pw[i % 8], cur4, q4, kv4, pe4, None,
+                                                     model_arch="deepseek_v3_2"), st, 5)
+    b = gemm_bytes(4, 2112, 7168)
+    fused_us = tot_us - per["wq_a"]["us"] - per["wkv_a"]["us"] + us
     out["mla_projections_M4"] = {"layers": per, "us_total": round(tot_us, 2),
                                  "GBs": round(tot_b / tot_us / 1e3, 1),
-                                 "hbm_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 3)}
+                                 "hbm_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 3),
+                                 "projx_wqkva": {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)},
+                                 "us_total_with_projx": round(fused_us, 2),
+                                 "hbm_frac_with_projx": round(tot_b / fused_us / 1e3 / HBM_PEAK_GBS, 3)}
 
     # config 3: M sweep on the dense MLP up / down (MFMA utilisation for M >= 64)
     sweep = {}

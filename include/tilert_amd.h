@@ -20,6 +20,7 @@
  *                       projx_wqkva_op (.../ops/projx_wqkva.py:22-48), rmsnorm_proj_qb_op,
  *                       unproj_o_allreduce_op, rmsnorm_up_gate_silu_op, down_allreduce_op
  *   tl_fp8_pack_weight  the per-op weight converters (load-time layout change)
+ *   tl_projx_wqkva      projx_wqkva_op       .../ops/projx_wqkva.py:22-48 (golden :268-294)
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
  *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
@@ -95,6 +96,24 @@ int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* 
 int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, const float* b_s,
                        void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/* The fused attention down-projection of one decode step: x_q . [wq_a; wkv_a]^T in one
+ * launch, its columns routed to three outputs.  x_q fp8 [batch*seq, dim] + x_s fp32
+ * [batch*seq, dim/128]; w_packed = tl_fp8_pack_weight of the row-stacked weight
+ * [q_rank + kv_rank + rope_dim, dim] (wq_a, then wkv_a = kv_a_proj_with_mqa: kv_rank latent
+ * rows, then rope_dim rope rows), w_s its fp32 block scales [ceil(N/128), dim/128] (wq_a's
+ * scale rows, then wkv_a's: q_rank % 128 == 0 makes the stack an ordinary block-scaled
+ * weight).  Outputs bf16: q_out [batch*seq, q_rank], kv_out [batch*seq, kv_rank], and the
+ * rope part written into pe_cache [batch, cache_rows, rope_dim] at row *cur_pos + s for
+ * token (b, s) (cur_pos: device int32, read by the kernel; rows outside [0, cache_rows)
+ * are not written).  Needs batch*seq <= 64, dim % 512 == 0, kv_rank and rope_dim multiples
+ * of 16, and the workspace of tl_fp8_gemm_workspace_bytes(batch*seq, N, dim).  Replaces
+ * projx_wqkva_op (tilert/models/deepseek_v3_2/ops/projx_wqkva.py:22-48; golden :268-294). */
+int tl_projx_wqkva(const void* x_q, const float* x_s, const void* w_packed, const float* w_s,
+                   const int32_t* cur_pos, void* q_out, void* kv_out, void* pe_cache,
+                   int64_t batch, int64_t seq, int64_t cache_rows, int64_t dim, int64_t q_rank,
+                   int64_t kv_rank, int64_t rope_dim, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /* Tile-major fragment packing for the MoE kernels: the stacked per-expert weights
  * [rows, K] (rows % 16 == 0, K % 128 == 0) become fragments (t, kb) at (t*K/128 + kb)*2048

@@ -140,6 +140,23 @@ def linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, scale_mode: int 
     return fp8_gemm(xq, xs, wq, ws)
 
 
+def projx_wqkva(x_q: torch.Tensor, x_s: torch.Tensor, wq_a: torch.Tensor, wq_a_s: torch.Tensor,
+                wkv_a: torch.Tensor, wkv_a_s: torch.Tensor, kv_lora_rank: int
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Golden of projx_wqkva (projx_wqkva.py:268-294): dequantise x per 1x128, dequantise
+    wq_a and kv_a_proj_with_mqa (whose first kv_lora_rank rows are the latent projection and
+    the rest w_pe, :195-196), three fp32 matmuls, each rounded to bf16 -> (q, kv, pe)."""
+    K = x_q.shape[-1]
+    xa = act_dequant(x_q.reshape(-1, K), x_s.reshape(-1, K // BLOCK))
+    wq = weight_dequant(wq_a, wq_a_s)
+    wkv = weight_dequant(wkv_a, wkv_a_s)
+    lead = x_q.shape[:-1]
+    q = (xa @ wq.T).to(torch.bfloat16).reshape(*lead, -1)
+    kv = (xa @ wkv[:kv_lora_rank].T).to(torch.bfloat16).reshape(*lead, -1)
+    pe = (xa @ wkv[kv_lora_rank:].T).to(torch.bfloat16).reshape(*lead, -1)
+    return q, kv, pe
+
+
 def swiglu(g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
     """``silu(g) * u`` in fp32 (expert_sel_up_gate_silu.py:687)."""
     return F.silu(g.float()) * u.float()

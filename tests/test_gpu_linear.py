@@ -60,7 +60,9 @@ def test_weight_quant_bit_exact(cuda, N, Kd):
 GEMM_CASES = [
     # (M, N, K)
     (1, 256, 512),
-    (4, 576, 7168),     # wkv_a: split-K + partial last scale row
+    (4, 576, 7168),     # wkv_a: partial last scale row
+    (32, 576, 7168),    # 36 row tiles at M > 16: split-K in 4 slices
+    (2, 7168, 6144),    # wide and long: 4 operand buffers per wave
     (4, 3072, 1536),    # wq_b
     (4, 4096, 512),     # wkv_b
     (4, 7168, 2048),    # wo
@@ -143,7 +145,7 @@ def test_fp8_gemm_rejects_bad_shapes(cuda):
         K.fp8_gemm(a, torch.zeros(4, 1, device=cuda), a, torch.zeros(1, 1, device=cuda))
 
 
-@pytest.mark.parametrize("M,N,Kd", [(4, 576, 7168), (4, 18432, 7168), (2, 7168, 2048), (64, 2048, 7168), (128, 2048, 7168)])
+@pytest.mark.parametrize("M,N,Kd", [(32, 576, 7168), (4, 18432, 7168), (2, 7168, 2048), (64, 2048, 7168), (128, 2048, 7168)])
 def test_fp8_gemm_split_k_repeatable(cuda, M, N, Kd):
     """The cross-workgroup split-K reduction must give bit-identical results on every
     call (a stale or missing partial would show up as a changed output)."""

@@ -88,6 +88,25 @@ def test_fp8_gemm_scale_linearity_and_transpose_sensitivity():
     assert torch.equal(out[:, :128], base[:, :128]) and not torch.equal(out[:, 128:], base[:, 128:])
 
 
+def test_projx_wqkva_parts_vs_fp64_brute_force():
+    """q, kv and pe are the three column ranges of x . [wq_a; wkv_a]^T: each is checked
+    against fp64 brute force over the whole of its weight (so a wrong latent/rope split
+    row or a shifted scale row fails)."""
+    g = synth.gen(77)
+    xq, xs = ref.act_quant(synth.activations(3, 256, g))
+    wq, wqs = ref.weight_quant(synth.weight_fp32(128, 256, g))
+    wkv, wkvs = ref.weight_quant(synth.weight_fp32(160, 256, g) * 3)  # 2 scale rows, the second partial
+    q, kv, pe = ref.projx_wqkva(xq, xs, wq, wqs, wkv, wkvs, kv_lora_rank=144)
+    assert q.shape == (3, 128) and kv.shape == (3, 144) and pe.shape == (3, 16)
+    xc, xsn = xq.view(torch.uint8).numpy(), xs.numpy()
+    want_q = brute.gemm_fp64(xc, xsn, wq.view(torch.uint8).numpy(), wqs.numpy())
+    want_kv = brute.gemm_fp64(xc, xsn, wkv.view(torch.uint8).numpy(), wkvs.numpy())
+    for got, want in ((q, want_q), (kv, want_kv[:, :144]), (pe, want_kv[:, 144:])):
+        got = got.double().numpy()
+        ulp = 2.0 ** (np.floor(np.log2(np.abs(want) + 1e-30)) - 7)
+        assert np.all(np.abs(got - want) <= 0.5 * ulp + 1e-6 * np.abs(want) + 1e-30)
+
+
 # ----------------------------------------------------------------------------- MoE
 def _tiny_experts(E, D, I, g):
     out = []

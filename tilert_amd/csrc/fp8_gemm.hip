@@ -68,10 +68,51 @@ __device__ inline size_t packed_fragment(int t, int kb, int NT) {
 // is requested one block ahead, so L2 latency of the activations hides behind the
 // current MFMA.  Staging activations in LDS instead was measured slower: its prologue
 // costs what it saves.
-template <int MT, int WAVES, bool PACKED>
+// Where the output lands.  Column n of row t goes to segment 0 (n < end0), 1
+// (n < end1) or 2, at column n - (segment start) of row t with the segment's leading
+// dimension; segment 2 may instead be a cache indexed by position: row
+// (t / seq) * cache_rows + *cur_pos + t % seq, skipped when that position is outside
+// [0, cache_rows).  A plain GEMM is one segment: C [M, N].  The 4 columns a lane stores
+// lie in one 16-column tile, so in one segment (segment bounds are multiples of 16).
+struct OutRoute {
+  uint16_t* p0;
+  uint16_t* p1;
+  uint16_t* p2;
+  int end0, end1;
+  int ld0, ld1, ld2;
+  const int32_t* cur_pos;  // null: segment 2 is a plain [M, ld2] matrix
+  int seq, cache_rows;
+};
+
+__host__ inline OutRoute plain_out(uint16_t* C, int N) {
+  return OutRoute{C, nullptr, nullptr, N, N, N, 0, 0, nullptr, 1, 0};
+}
+
+__device__ inline void store_out(const OutRoute& o, int t, int n, uint2 v) {
+  uint16_t* dst;
+  if (n < o.end0) {
+    dst = o.p0 + static_cast<size_t>(t) * o.ld0 + n;
+  } else if (n < o.end1) {
+    dst = o.p1 + static_cast<size_t>(t) * o.ld1 + (n - o.end0);
+  } else {
+    int row = t;
+    if (o.cur_pos) {
+      const int pos = *o.cur_pos + t % o.seq;
+      if (pos < 0 || pos >= o.cache_rows) return;
+      row = (t / o.seq) * o.cache_rows + pos;
+    }
+    dst = o.p2 + static_cast<size_t>(row) * o.ld2 + (n - o.end1);
+  }
+  *reinterpret_cast<uint2*>(dst) = v;
+}
+
+// D: operand buffers per wave.  D = 2 is the ping-pong below; narrow layers (few row
+// tiles, so few waves on the chip) take a deeper ring so that enough weight bytes are in
+// flight to cover HBM latency without splitting K.
+template <int MT, int WAVES, bool PACKED, int D = 2>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
-    const float* __restrict__ Bs, uint16_t* __restrict__ C, float* __restrict__ partial,
+    const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
   __shared__ float red[WAVES - 1][MT][4][64];
   const int KB = K >> 7;
@@ -129,22 +170,28 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   // this wave's K blocks: kb_begin + wv + i*WAVES, i < n
   const int kb0 = kb_begin + wv;
   const int n = kb0 < kb_end ? (kb_end - kb0 + WAVES - 1) / WAVES : 0;
-  Ops b0, b1;
-  if (n > 0) {
-    fetch(kb0, b0);
-    int i = 0;
-    for (; i + 2 < n; i += 2) {
-      fetch(kb0 + (i + 1) * WAVES, b1);
-      compute(b0);
-      fetch(kb0 + (i + 2) * WAVES, b0);
-      compute(b1);
-    }
-    if (i + 1 < n) {
-      fetch(kb0 + (i + 1) * WAVES, b1);
-      compute(b0);
-      compute(b1);
-    } else {
-      compute(b0);
+  if constexpr (D > 2) {
+    Ops ring[D];
+    ring_pipeline<D>(n, ring, [&](int i, Ops& o) { fetch(kb0 + i * WAVES, o); },
+                     [&](int, const Ops& o) { compute(o); });
+  } else {
+    Ops b0, b1;
+    if (n > 0) {
+      fetch(kb0, b0);
+      int i = 0;
+      for (; i + 2 < n; i += 2) {
+        fetch(kb0 + (i + 1) * WAVES, b1);
+        compute(b0);
+        fetch(kb0 + (i + 2) * WAVES, b0);
+        compute(b1);
+      }
+      if (i + 1 < n) {
+        fetch(kb0 + (i + 1) * WAVES, b1);
+        compute(b0);
+        compute(b1);
+      } else {
+        compute(b0);
+      }
     }
   }
 
@@ -170,7 +217,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int t = mt * 16 + r;
-      if (t < M) *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(acc[mt]);
+      if (t < M) store_out(out, t, ncol, pack_bf16x4(acc[mt]));
     }
     return;
   }
@@ -212,7 +259,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
         for (int u = 0; u < 8; ++u)
           if (q0 + u < ksplit) s += v[u];
       }
-      *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(s);
+      store_out(out, t, ncol, pack_bf16x4(s));
     }
   }
   if (lane == 0) __hip_atomic_store(&counters[rt], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -303,7 +350,7 @@ constexpr int tiled_lds_bytes() { return TiledShape<TT>::LDS; }
 template <int TT, bool PACKED>
 __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
-    const float* __restrict__ Bs, uint16_t* __restrict__ C, float* __restrict__ partial,
+    const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
   using S = TiledShape<TT>;
   constexpr int KC = S::KC, D = kTiledDepth, THREADS = S::THREADS;
@@ -436,7 +483,7 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
         const int t = tt * 16 + r;
-        if (t < M) *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(acc[tt]);
+        if (t < M) store_out(out, t, ncol, pack_bf16x4(acc[tt]));
       }
     }
     return;
@@ -480,7 +527,7 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
           for (int u = 0; u < 8; ++u)
             if (q0 + u < ksplit) s += v[u];
         }
-        *reinterpret_cast<uint2*>(C + static_cast<size_t>(t) * N + ncol) = pack_bf16x4(s);
+        store_out(out, t, ncol, pack_bf16x4(s));
       }
     }
   }
@@ -493,13 +540,15 @@ struct GemmPlan {
   int kb_per_split;
   int row_groups;  // grid.x: 16-row tiles (GEMV) or 128-row groups (tiled)
   int waves;
+  int depth;  // GEMV operand buffers per wave
 };
 
-// K split.  GEMV (M <= 16): wide layers (>= 512 row tiles, i.e. >= 2 workgroups per CU)
-// run unsplit: measured on MI355X, the split's extra round trips (partial store, counter,
-// reload) cost more than the better CU balance buys.  Narrow layers take the smallest
-// split giving >= 1024 workgroups (4 per CU), preferring a grid that is a whole multiple
-// of the 256 CUs, with slices of whole K groups, never leaving a slice empty.
+// K split.  GEMV (M <= 16): never split.  Measured on MI355X at every MLA, MLP and
+// MoE-sized layer, the split's extra round trips (partial store, counter, reload: ~2 us)
+// cost more than the extra CUs buy -- even a 36-tile layer, whose workgroups each stream
+// 114 KB, is faster unsplit (5.6 vs 7.7 us).  M = 17..64: a layer of fewer than 192 row
+// tiles splits K into cdiv(256, tiles) <= 4 slices of whole K groups (there the activation
+// reads make a workgroup's work long enough for the split to pay); wider layers do not.
 // Tiled (M > 64; measured faster than the per-row-tile kernel from M = 128 on, slower at
 // M = 32 and 64): the smallest split giving >= 512 workgroups (2 per CU) with slices of
 // at least 8 K blocks.
@@ -507,6 +556,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
   p.tiled = M > 64;
+  p.depth = 2;
   if (p.tiled) {
     p.row_groups = static_cast<int>(cdiv(N / 16, kTiledWaves));
     int s = static_cast<int>(cdiv(512, p.row_groups));
@@ -519,19 +569,14 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   const int groups = static_cast<int>(cdiv(KB, kGroup));
   p.row_groups = static_cast<int>(N / 16);
   int s = 1;
-  if (p.row_groups < 512) {
-    int smin = static_cast<int>(cdiv(1024, p.row_groups));
-    if (smin > groups) smin = groups;
-    if (smin < 1) smin = 1;
-    s = smin;
-    for (int c = smin; c <= 2 * smin && c <= groups; ++c) {
-      if ((static_cast<int64_t>(p.row_groups) * c) % 256 == 0) { s = c; break; }
-    }
-  }
+  if (M > 16 && p.row_groups < 192) s = std::max(1, std::min({4, groups, static_cast<int>(cdiv(256, p.row_groups))}));
   p.kb_per_split = static_cast<int>(cdiv(groups, s)) * kGroup;
   p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
-  // wide layers: 8 waves (two K groups per step); split slices: 4 (one group)
-  p.waves = (p.ksplit == 1 && KB >= 32) ? 8 : kGroup;
+  // unsplit layers: 8 waves (4 for K < 1024, where 8 would leave waves idle); split: 4
+  p.waves = (p.ksplit == 1 && KB >= 8) ? 8 : kGroup;
+  // long, wide GEMVs keep 4 K blocks in flight per wave (measured ~1% faster on the
+  // 7168 x 18432 and 18432 x 7168 layers; no gain on narrow ones)
+  if (M <= 16 && p.waves == 8 && KB >= 48 && p.row_groups >= 448) p.depth = 4;
   return p;
 }
 
@@ -543,7 +588,7 @@ constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 
 template <bool PACKED>
 static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, const float* Bs,
-                       uint16_t* C, int M, int N, int K, void* workspace, hipStream_t st) {
+                       const OutRoute& out, int M, int N, int K, void* workspace, hipStream_t st) {
   const GemmPlan p = plan_gemm(M, N, K);
   uint32_t* counters = p.ksplit > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
   float* partial = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
@@ -558,15 +603,17 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
         if (rc) return rc;
       }
       hipLaunchKernelGGL((fp8_gemm_tiled_kernel<TT, PACKED>), grid, dim3(kTiledWaves * 64), tiled_lds_bytes<TT>(), st,
-                         A, As, B, Bs, C, partial, counters, M, N, K, per);
+                         A, As, B, Bs, out, partial, counters, M, N, K, per);
       return check_launch("fp8_gemm");
     };
     if (M <= 128) return launch(std::integral_constant<int, 8>{});
     return launch(std::integral_constant<int, 16>{});
   }
 #define TL_GEMM_LAUNCH(MT, W) \
-  hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, C, partial, counters, M, N, K, per)
-  if (p.waves == 8) {
+  hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per)
+  if (p.depth == 4) {
+    hipLaunchKernelGGL((fp8_gemm_kernel<1, 8, PACKED, 4>), grid, dim3(8 * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per);
+  } else if (p.waves == 8) {
     if (M <= 16) TL_GEMM_LAUNCH(1, 8);
     else if (M <= 32) TL_GEMM_LAUNCH(2, 8);
     else TL_GEMM_LAUNCH(4, 8);
@@ -614,7 +661,7 @@ extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const
   const size_t need = tl_fp8_gemm_workspace_bytes(M, N, K);
   int rc = validate("fp8_gemm", a, a_s, b, b_s, c_bf16, M, N, K, workspace, workspace_bytes, need);
   if (rc) return rc;
-  return launch_gemm<false>((const uint8_t*)a, a_s, (const uint8_t*)b, b_s, (uint16_t*)c_bf16,
+  return launch_gemm<false>((const uint8_t*)a, a_s, (const uint8_t*)b, b_s, plain_out((uint16_t*)c_bf16, (int)N),
                             (int)M, (int)N, (int)K, workspace, (hipStream_t)stream);
 }
 
@@ -646,6 +693,39 @@ extern "C" int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b
   const size_t need = tl_fp8_gemm_workspace_bytes(M, N, K);
   int rc = validate("fp8_gemm_packed", a, a_s, b_packed, b_s, c_bf16, M, N, K, workspace, workspace_bytes, need);
   if (rc) return rc;
-  return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, (uint16_t*)c_bf16,
+  return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, plain_out((uint16_t*)c_bf16, (int)N),
                            (int)M, (int)N, (int)K, workspace, (hipStream_t)stream);
+}
+
+extern "C" int tl_projx_wqkva(const void* x_q, const float* x_s, const void* w_packed,
+                              const float* w_s, const int32_t* cur_pos, void* q_out, void* kv_out,
+                              void* pe_cache, int64_t batch, int64_t seq, int64_t cache_rows,
+                              int64_t dim, int64_t q_rank, int64_t kv_rank, int64_t rope_dim,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  const char* who = "projx_wqkva";
+  if (batch <= 0 || seq <= 0 || cache_rows <= 0 || q_rank <= 0 || kv_rank <= 0 || rope_dim <= 0) {
+    set_error("%s: batch, seq, cache rows and the three output widths must be positive", who);
+    return kErrArg;
+  }
+  if (q_rank % kBlock || kv_rank % 16 || rope_dim % 16) {
+    set_error("%s: q_rank must be a multiple of 128 and kv_rank, rope_dim of 16 (got %lld, %lld, %lld)", who,
+              (long long)q_rank, (long long)kv_rank, (long long)rope_dim);
+    return kErrArg;
+  }
+  if (dim % (kBlock * kGroup)) { set_error("%s: dim=%lld must be a multiple of 512", who, (long long)dim); return kErrArg; }
+  const int64_t M = batch * seq, N = q_rank + kv_rank + rope_dim;
+  if (M > 64) { set_error("%s: batch*seq=%lld > 64 is not supported (decode GEMV)", who, (long long)M); return kErrUnsupported; }
+  if (!cur_pos || !kv_out || !pe_cache) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(kv_out) | reinterpret_cast<uintptr_t>(pe_cache)) & 7) {
+    set_error("%s: outputs must be 8-byte aligned", who);
+    return kErrArg;
+  }
+  if (cache_rows > (1ll << 30) / rope_dim) { set_error("%s: cache too large", who); return kErrArg; }
+  const size_t need = tl_fp8_gemm_workspace_bytes(M, N, dim);
+  int rc = validate(who, x_q, x_s, w_packed, w_s, q_out, M, N, dim, workspace, workspace_bytes, need);
+  if (rc) return rc;
+  OutRoute out{(uint16_t*)q_out, (uint16_t*)kv_out, (uint16_t*)pe_cache, (int)q_rank, (int)(q_rank + kv_rank),
+               (int)q_rank, (int)kv_rank, (int)rope_dim, cur_pos, (int)seq, (int)cache_rows};
+  return launch_gemm<true>((const uint8_t*)x_q, x_s, (const uint8_t*)w_packed, w_s, out, (int)M, (int)N,
+                           (int)dim, workspace, (hipStream_t)stream);
 }
