@@ -76,6 +76,13 @@ GEMM_CASES = [
     (32, 1152, 2048),
     (200, 400, 2048),   # 25 row tiles: a partly empty last 128-row group
     (100, 7168, 1024),
+    # several row tiles per workgroup sharing each activation fragment
+    (16, 7168, 1024),   # 2 row tiles, 1 token tile
+    (16, 7168, 640),    # the same on the canonical (unpacked) layout
+    (32, 18432, 512),   # 4 row tiles, 2 token tiles
+    (24, 6144, 512),    # 2 row tiles, 2 token tiles
+    (48, 7168, 1024),   # 2 row tiles, 4 token tiles
+    (64, 12288, 512),   # 4 row tiles, 4 token tiles
 ]
 
 

@@ -109,48 +109,53 @@ __device__ inline void store_out(const OutRoute& o, int t, int n, uint2 v) {
 // D: operand buffers per wave.  D = 2 is the ping-pong below; narrow layers (few row
 // tiles, so few waves on the chip) take a deeper ring so that enough weight bytes are in
 // flight to cover HBM latency without splitting K.
-template <int MT, int WAVES, bool PACKED, int D = 2>
+// RT: 16-row tiles per workgroup (1, 2 or 4; within one 128-row scale block).  Each
+// activation fragment a wave loads then serves RT weight fragments, which divides the
+// activation traffic (as large as the weight traffic itself from M = 16 on) by RT.
+template <int MT, int WAVES, bool PACKED, int D = 2, int RT = 1>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
-  __shared__ float red[WAVES - 1][MT][4][64];
+  constexpr int NA = RT * MT;  // accumulators per lane: (row tile j, token tile mt) at j * MT + mt
+  __shared__ float red[WAVES - 1][NA][4][64];
   const int KB = K >> 7;
   const int NT = N >> 4;
   const int ksplit = gridDim.y;
   const int ks = blockIdx.y;
   const int kb_begin = ks * kb_per_split;
   const int kb_end = min(KB, kb_begin + kb_per_split);
-  const int rt = blockIdx.x;
+  const int rt = blockIdx.x * RT;  // first row tile
   const int n0 = rt * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
 
   const uint8_t* brow = B + static_cast<size_t>(n0 + r) * K;  // canonical layout
   const float* bs_row = Bs + static_cast<size_t>(n0 >> 7) * KB;
-  auto load_w = [&](int kb) -> v8i {
-    return PACKED ? load_packed_fragment(B + packed_fragment(rt, kb, NT), lane)
-                  : load_kblock_stream(brow + static_cast<size_t>(kb) * kBlock, g);
+  auto load_w = [&](int kb, int j) -> v8i {
+    return PACKED ? load_packed_fragment(B + packed_fragment(rt + j, kb, NT), lane)
+                  : load_kblock_stream(brow + static_cast<size_t>(16 * j) * K + static_cast<size_t>(kb) * kBlock, g);
   };
   // Activation rows past M are read from row M-1 and zeroed afterwards, so every load
   // in the loop below is unconditional: the compiler's wait-count pass can then wait for
   // exactly the operands an MFMA needs instead of for everything in flight.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
 
-  v4f acc[MT];
+  v4f acc[NA];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NA; ++i) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // Ping-pong over two operand buffers (the loop is unrolled by two) so the next K
   // block's loads are in flight during this block's MFMAs.  A `cur = next` rotation
   // would make the compiler copy registers at the end of each iteration -- and wait for
   // the loads in flight to do so, serialising the stream.
   struct Ops {
-    v8i a, x[MT];
+    v8i a[RT], x[MT];
     float xs[MT], bs;
   };
   auto fetch = [&](int kb, Ops& o) {
-    o.a = load_w(kb);
+#pragma unroll
+    for (int j = 0; j < RT; ++j) o.a[j] = load_w(kb, j);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int t = min(mt * 16 + r, M - 1);
@@ -164,7 +169,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const float xs = mt * 16 + r < M ? o.xs[mt] : 0.f;  // zero rows past M
-      acc[mt] += mfma_16x16x128_fp8(o.a, o.x[mt]) * (o.bs * xs);
+#pragma unroll
+      for (int j = 0; j < RT; ++j) acc[j * MT + mt] += mfma_16x16x128_fp8(o.a[j], o.x[mt]) * (o.bs * xs);
     }
   };
   // this wave's K blocks: kb_begin + wv + i*WAVES, i < n
@@ -198,26 +204,25 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   // ---- cross-wave reduction in fixed order w0 + w1 + ... + w(WAVES-1)
   if (wave > 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int i = 0; i < NA; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave - 1][mt][j][lane] = acc[mt][j];
+      for (int j = 0; j < 4; ++j) red[wave - 1][i][j][lane] = acc[i][j];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int i = 0; i < NA; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[mt][j] += red[w][mt][j][lane];
+      for (int j = 0; j < 4; ++j) acc[i][j] += red[w][i][j][lane];
 
-  // lane holds output columns n0 + 4g + j (j = 0..3) of token mt*16 + r
-  const int ncol = n0 + 4 * g;
+  // lane holds output columns n0 + 16 jt + 4g + j (j = 0..3) of token mt*16 + r
   if (ksplit == 1) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int t = mt * 16 + r;
-      if (t < M) store_out(out, t, ncol, pack_bf16x4(acc[mt]));
+    for (int i = 0; i < NA; ++i) {
+      const int t = (i % MT) * 16 + r;
+      if (t < M) store_out(out, t, n0 + 16 * (i / MT) + 4 * g, pack_bf16x4(acc[i]));
     }
     return;
   }
@@ -227,12 +232,12 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   // coherence point, read past this XCD's L2), so no cache-wide writeback or
   // invalidate is needed; s_waitcnt makes the stores complete before the counter bump.
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int t = mt * 16 + r;
+  for (int i = 0; i < NA; ++i) {
+    const int t = (i % MT) * 16 + r;
     if (t < M) {
-      float* dst = partial + (static_cast<size_t>(ks) * M + t) * N + ncol;
+      float* dst = partial + (static_cast<size_t>(ks) * M + t) * N + n0 + 16 * (i / MT) + 4 * g;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) __hip_atomic_store(dst + j, acc[mt][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int j = 0; j < 4; ++j) __hip_atomic_store(dst + j, acc[i][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -241,8 +246,9 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   prev = __shfl(prev, 0);
   if (prev != static_cast<uint32_t>(ksplit - 1)) return;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int t = mt * 16 + r;
+  for (int i = 0; i < NA; ++i) {
+    const int t = (i % MT) * 16 + r;
+    const int ncol = n0 + 16 * (i / MT) + 4 * g;
     if (t < M) {
       // issue the loads of 8 slices at a time, then add them in slice order
       v4f s = {0.f, 0.f, 0.f, 0.f};
@@ -541,6 +547,7 @@ struct GemmPlan {
   int row_groups;  // grid.x: 16-row tiles (GEMV) or 128-row groups (tiled)
   int waves;
   int depth;  // GEMV operand buffers per wave
+  int rt;     // GEMV row tiles per workgroup
 };
 
 // K split.  GEMV (M <= 16): never split.  Measured on MI355X at every MLA, MLP and
@@ -557,6 +564,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   const int KB = static_cast<int>(K / kBlock);
   p.tiled = M > 64;
   p.depth = 2;
+  p.rt = 1;
   if (p.tiled) {
     p.row_groups = static_cast<int>(cdiv(N / 16, kTiledWaves));
     int s = static_cast<int>(cdiv(512, p.row_groups));
@@ -577,6 +585,17 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   // long, wide GEMVs keep 4 K blocks in flight per wave (measured ~1% faster on the
   // 7168 x 18432 and 18432 x 7168 layers; no gain on narrow ones)
   if (M <= 16 && p.waves == 8 && KB >= 48 && p.row_groups >= 448) p.depth = 4;
+  // From M = 5 on, each activation fragment serves 2 or 4 row tiles (measured: up
+  // 7168 -> 18432 at M = 16 / 32 / 64: 33.2 -> 28.7 / 53.7 -> 40.8 / 103.7 -> 68.3 us; down
+  // 18432 -> 7168 at M = 16 / 64: 35.2 -> 26.8 / 103.1 -> 59.8 us; at M = 4 it is 1 us
+  // slower), keeping >= 192 workgroups; 4 row tiles only from M = 17 on (slower at 16).
+  if (M > 4 && p.ksplit == 1 && p.waves == 8) {
+    const int want = M > 16 ? 4 : 2;
+    for (int rt = want; rt > 1; rt /= 2) {
+      if (p.row_groups % rt == 0 && p.row_groups / rt >= 192) { p.rt = rt; break; }
+    }
+    if (p.rt > 1) p.depth = 2;
+  }
   return p;
 }
 
@@ -592,7 +611,7 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
   const GemmPlan p = plan_gemm(M, N, K);
   uint32_t* counters = p.ksplit > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
   float* partial = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
-  const dim3 grid(p.row_groups, p.ksplit);
+  const dim3 grid(p.row_groups / p.rt, p.ksplit);
   const int per = p.kb_per_split;
   if (p.tiled) {
     auto launch = [&](auto tt_tag) -> int {
@@ -611,7 +630,19 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
   }
 #define TL_GEMM_LAUNCH(MT, W) \
   hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per)
-  if (p.depth == 4) {
+  if (p.rt > 1) {
+#define TL_GEMM_LAUNCH_RT(MT, RT) \
+  hipLaunchKernelGGL((fp8_gemm_kernel<MT, 8, PACKED, 2, RT>), grid, dim3(8 * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per)
+    if (p.rt == 2) {
+      if (M <= 16) TL_GEMM_LAUNCH_RT(1, 2);
+      else if (M <= 32) TL_GEMM_LAUNCH_RT(2, 2);
+      else TL_GEMM_LAUNCH_RT(4, 2);
+    } else {
+      if (M <= 32) TL_GEMM_LAUNCH_RT(2, 4);
+      else TL_GEMM_LAUNCH_RT(4, 4);
+    }
+#undef TL_GEMM_LAUNCH_RT
+  } else if (p.depth == 4) {
     hipLaunchKernelGGL((fp8_gemm_kernel<1, 8, PACKED, 4>), grid, dim3(8 * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per);
   } else if (p.waves == 8) {
     if (M <= 16) TL_GEMM_LAUNCH(1, 8);
