@@ -69,9 +69,10 @@ int tl_weight_dequant(const void* q_fp8, const float* s, void* out, int out_bf16
 /* c[M,N] bf16 = (a . b^T) with per-128-K-block scaling, fp32 accumulation.
  * a fp8 [M,K], a_s fp32 [M,K/128], b fp8 [N,K], b_s fp32 [ceil(N/128),K/128].
  * Requires K % 128 == 0, N % 16 == 0, 1 <= M <= 256, 16-byte aligned a and b.
- * Narrow problems split K across workgroups and need a workspace of
- * tl_fp8_gemm_workspace_bytes(M,N,K) bytes, ZERO-FILLED before its first use; the kernel
- * leaves it ready for the next call.  Calls that share a workspace must be ordered
+ * From M = 16 on (a rearranged copy of the activations) and for narrow layers at
+ * M > 16 (split-K partials) the call needs a workspace of tl_fp8_gemm_workspace_bytes(M,N,K)
+ * bytes (0 = none), ZERO-FILLED before its first use; the kernels leave it ready for the
+ * next call.  Calls that share a workspace must be ordered
  * (same stream).  Replaces fp8_gemm (refs/kernel.py:282-306). */
 size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s, void* c_bf16,

@@ -56,6 +56,7 @@ def test_argument_errors_need_no_gpu():
     assert lib.tl_fp8_gemm_workspace_bytes(32, 576, 7168) > 0  # narrow layer at M > 16: split K
     assert lib.tl_fp8_gemm_workspace_bytes(4, 576, 7168) == 0  # GEMV: never split
     assert lib.tl_fp8_gemm_workspace_bytes(4, 18432, 7168) == 0
+    assert lib.tl_fp8_gemm_workspace_bytes(16, 18432, 7168) > 0  # activation image
     # projx_wqkva: q_rank not a multiple of 128, then more than 64 tokens
     assert lib.tl_projx_wqkva(None, None, None, None, None, None, None, None, 1, 4, 128, 7168, 1000, 512, 64, None, 0, None) == 1
     assert lib.tl_projx_wqkva(None, None, None, None, None, None, None, None, 2, 40, 128, 7168, 1536, 512, 64, None, 0, None) == 3

@@ -46,6 +46,14 @@ __device__ inline v8i load_packed_fragment(const uint8_t* frag, int lane) {
   return r;
 }
 
+// The same fragment through the caches (activation images are re-read by every workgroup).
+__device__ inline v8i load_fragment(const uint8_t* frag, int lane) {
+  const uint4 lo = reinterpret_cast<const uint4*>(frag)[lane];
+  const uint4 hi = reinterpret_cast<const uint4*>(frag)[64 + lane];
+  return v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+             static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+}
+
 __device__ inline uint2 pack_bf16x4(v4f v) {
   return make_uint2(f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16),
                     f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16));
@@ -112,7 +120,9 @@ __device__ inline void store_out(const OutRoute& o, int t, int n, uint2 v) {
 // RT: 16-row tiles per workgroup (1, 2 or 4; within one 128-row scale block).  Each
 // activation fragment a wave loads then serves RT weight fragments, which divides the
 // activation traffic (as large as the weight traffic itself from M = 16 on) by RT.
-template <int MT, int WAVES, bool PACKED, int D = 2, int RT = 1>
+// XF: A / As are the activation image of act_image_kernel (fragment order, transposed
+// scales) instead of x [M, K] / [M, K/128].
+template <int MT, int WAVES, bool PACKED, int D = 2, int RT = 1, bool XF = false>
 __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
@@ -158,9 +168,15 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     for (int j = 0; j < RT; ++j) o.a[j] = load_w(kb, j);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int t = min(mt * 16 + r, M - 1);
-      o.x[mt] = load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g);
-      o.xs[mt] = As[static_cast<size_t>(t) * KB + kb];
+      if constexpr (XF) {
+        const int mtt = (M + 15) >> 4;
+        o.x[mt] = load_fragment(A + (static_cast<size_t>(kb) * mtt + mt) * 2048, lane);
+        o.xs[mt] = As[static_cast<size_t>(kb) * mtt * 16 + mt * 16 + r];
+      } else {
+        const int t = min(mt * 16 + r, M - 1);
+        o.x[mt] = load_kblock(A + static_cast<size_t>(t) * K + kb * kBlock, g);
+        o.xs[mt] = As[static_cast<size_t>(t) * KB + kb];
+      }
     }
     o.bs = bs_row[kb];
     __builtin_amdgcn_sched_barrier(0);  // keep the loads issued ahead of the MFMAs after them
@@ -289,6 +305,38 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint8_t* __restr
   const int col = kb * 128 + 64 * p + 16 * (l >> 4);
   *reinterpret_cast<uint4*>(P + packed_fragment(t, kb, NT) + within * 16) =
       *reinterpret_cast<const uint4*>(W + static_cast<size_t>(row) * K + col);
+}
+
+// Activation image for the GEMVs at M > 16: x [M, K] rearranged so that the MFMA operand
+// of token tile tt and K block kb is 2 KB of consecutive memory at (kb * MTT + tt) * 2048
+// (MTT = ceil(M / 16); in-fragment order as in the weight packing; tokens past M repeat
+// token M-1), and the scales transposed to [K/128, 16 MTT] (0 past M).  The GEMV's
+// activation loads then become contiguous 1 KB reads.  The gather they replace (16 rows x
+// 64 B per instruction) was measured at ~9 TB/s of L2-resident reads across the chip,
+// against ~33 TB/s for contiguous ones.
+__global__ __launch_bounds__(256) void act_image_kernel(const uint8_t* __restrict__ A, const float* __restrict__ As,
+                                                        uint8_t* __restrict__ X, float* __restrict__ Xs, int M, int K) {
+  const int KB = K >> 7;
+  const int mtt = (M + 15) >> 4;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < static_cast<int64_t>(KB) * mtt * 128) {  // one 16-byte chunk per thread
+    const int64_t frag = i >> 7;
+    const int within = static_cast<int>(i & 127);
+    const int p = within >> 6, l = within & 63;
+    const int kb = static_cast<int>(frag / mtt), tt = static_cast<int>(frag % mtt);
+    const int row = min(tt * 16 + (l & 15), M - 1);
+    *reinterpret_cast<uint4*>(X + i * 16) =
+        *reinterpret_cast<const uint4*>(A + static_cast<size_t>(row) * K + kb * 128 + 64 * p + 16 * (l >> 4));
+  }
+  if (i < static_cast<int64_t>(KB) * mtt * 16) {  // one scale per thread
+    const int kb = static_cast<int>(i / (mtt * 16)), t = static_cast<int>(i % (mtt * 16));
+    Xs[i] = t < M ? As[static_cast<size_t>(t) * KB + kb] : 0.f;
+  }
+}
+
+__host__ inline size_t act_image_bytes(int64_t M, int64_t K) {
+  const int64_t mtt = cdiv(M, 16), KB = K / kBlock;
+  return static_cast<size_t>(KB * mtt * 2048 + KB * mtt * 16 * 4);
 }
 
 // Tile-major fragment packing used by the MoE kernels: fragment (t, kb) at
@@ -548,6 +596,7 @@ struct GemmPlan {
   int waves;
   int depth;  // GEMV operand buffers per wave
   int rt;     // GEMV row tiles per workgroup
+  bool xf;    // GEMV reads the activation image (act_image_kernel) from the workspace
 };
 
 // K split.  GEMV (M <= 16): never split.  Measured on MI355X at every MLA, MLP and
@@ -565,6 +614,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
   p.tiled = M > 64;
   p.depth = 2;
   p.rt = 1;
+  p.xf = false;
   if (p.tiled) {
     p.row_groups = static_cast<int>(cdiv(N / 16, kTiledWaves));
     int s = static_cast<int>(cdiv(512, p.row_groups));
@@ -596,6 +646,10 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
     }
     if (p.rt > 1) p.depth = 2;
   }
+  // The activation image costs a launch: measured worth it from M = 16 on (M = 16 up /
+  // down: 28.7 -> 27.2 / 26.7 -> 25.9 us; M = 64: 68.4 -> 51.9 / 59.9 -> 43.0 us), not at
+  // M = 8 (25.3 -> 27.7 us).
+  p.xf = M > 16 || (M == 16 && p.rt == 2);
   return p;
 }
 
@@ -604,6 +658,12 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
 // fixed region keeps one problem's partials from ever landing on another's counters.
 constexpr int kMaxRowTiles = 16384;  // N <= 262144
 constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
+
+// Workspace: counters, then the split-K partials, then the activation image (256-aligned).
+static size_t image_offset(const GemmPlan& p, int64_t M, int64_t N) {
+  const size_t partial = p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
+  return kCounterBytes + (partial + 255) / 256 * 256;
+}
 
 template <bool PACKED>
 static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, const float* Bs,
@@ -628,32 +688,52 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
     if (M <= 128) return launch(std::integral_constant<int, 8>{});
     return launch(std::integral_constant<int, 16>{});
   }
-#define TL_GEMM_LAUNCH(MT, W) \
-  hipLaunchKernelGGL((fp8_gemm_kernel<MT, W, PACKED>), grid, dim3(W * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per)
-  if (p.rt > 1) {
-#define TL_GEMM_LAUNCH_RT(MT, RT) \
-  hipLaunchKernelGGL((fp8_gemm_kernel<MT, 8, PACKED, 2, RT>), grid, dim3(8 * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per)
-    if (p.rt == 2) {
-      if (M <= 16) TL_GEMM_LAUNCH_RT(1, 2);
-      else if (M <= 32) TL_GEMM_LAUNCH_RT(2, 2);
-      else TL_GEMM_LAUNCH_RT(4, 2);
-    } else {
-      if (M <= 32) TL_GEMM_LAUNCH_RT(2, 4);
-      else TL_GEMM_LAUNCH_RT(4, 4);
-    }
-#undef TL_GEMM_LAUNCH_RT
-  } else if (p.depth == 4) {
-    hipLaunchKernelGGL((fp8_gemm_kernel<1, 8, PACKED, 4>), grid, dim3(8 * 64), 0, st, A, As, B, Bs, out, partial, counters, M, N, K, per);
-  } else if (p.waves == 8) {
-    if (M <= 16) TL_GEMM_LAUNCH(1, 8);
-    else if (M <= 32) TL_GEMM_LAUNCH(2, 8);
-    else TL_GEMM_LAUNCH(4, 8);
-  } else {
-    if (M <= 16) TL_GEMM_LAUNCH(1, 4);
-    else if (M <= 32) TL_GEMM_LAUNCH(2, 4);
-    else TL_GEMM_LAUNCH(4, 4);
+  // GEMV.  M > 16 first rearranges the activations into the workspace (act_image_kernel).
+  const uint8_t* xa = A;
+  const float* xsa = As;
+  if (p.xf) {
+    uint8_t* img = static_cast<uint8_t*>(workspace) + image_offset(p, M, N);
+    const int64_t KB = K / kBlock, mtt = cdiv(M, 16);
+    float* img_s = reinterpret_cast<float*>(img + KB * mtt * 2048);
+    hipLaunchKernelGGL(act_image_kernel, dim3(static_cast<unsigned>(cdiv(KB * mtt * 128, 256))), dim3(256), 0, st,
+                       A, As, img, img_s, M, K);
+    xa = img;
+    xsa = img_s;
   }
-#undef TL_GEMM_LAUNCH
+  auto gemv = [&](auto mt, auto w, auto d, auto rt, auto xf) {
+    hipLaunchKernelGGL((fp8_gemm_kernel<decltype(mt)::value, decltype(w)::value, PACKED, decltype(d)::value,
+                                        decltype(rt)::value, decltype(xf)::value>),
+                       grid, dim3(decltype(w)::value * 64), 0, st, xa, xsa, B, Bs, out, partial, counters, M, N, K, per);
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  using F = std::false_type;
+  using T = std::true_type;
+  // token tiles 2 or 4 (M > 16), with or without the activation image
+  auto gemv_mt = [&](auto w, auto rt) {
+    if (M <= 32) {
+      if (p.xf) gemv(I2{}, w, I2{}, rt, T{}); else gemv(I2{}, w, I2{}, rt, F{});
+    } else {
+      if (p.xf) gemv(I4{}, w, I2{}, rt, T{}); else gemv(I4{}, w, I2{}, rt, F{});
+    }
+  };
+  if (M <= 16) {
+    if (p.rt == 2 && p.xf) gemv(I1{}, I8{}, I2{}, I2{}, T{});
+    else if (p.rt == 2) gemv(I1{}, I8{}, I2{}, I2{}, F{});
+    else if (p.depth == 4) gemv(I1{}, I8{}, I4{}, I1{}, F{});
+    else if (p.waves == 8) gemv(I1{}, I8{}, I2{}, I1{}, F{});
+    else gemv(I1{}, I4{}, I2{}, I1{}, F{});
+  } else if (p.rt == 4) {
+    gemv_mt(I8{}, I4{});
+  } else if (p.rt == 2) {
+    gemv_mt(I8{}, I2{});
+  } else if (p.waves == 8) {
+    gemv_mt(I8{}, I1{});
+  } else {
+    gemv_mt(I4{}, I1{});
+  }
   return check_launch("fp8_gemm");
 }
 
@@ -682,8 +762,8 @@ using namespace tl;
 extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock || M > 256) return 0;
   const GemmPlan p = plan_gemm(M, N, K);
-  if (p.ksplit == 1) return 0;
-  return kCounterBytes + static_cast<size_t>(p.ksplit) * M * N * sizeof(float);
+  if (p.ksplit == 1 && !p.xf) return 0;
+  return image_offset(p, M, N) + (p.xf ? act_image_bytes(M, K) : 0);
 }
 
 extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
