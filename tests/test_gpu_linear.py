@@ -101,7 +101,11 @@ def test_fp8_gemm_vs_oracle(cuda, M, N, Kd):
     if Kd % 512 == 0:
         packed = K.pack_weight(wq.to(cuda), ws.to(cuda))
         outp = K.fp8_gemm(xq.to(cuda), xs.to(cuda), packed)
-        assert torch.equal(outp, out), "packed-weight GEMM differs from the canonical one"
+        if M <= 64:  # the same GEMV kernel on both layouts
+            assert torch.equal(outp, out), "packed-weight GEMM differs from the canonical one"
+        else:  # M > 64: the MFMA GEMM (packed) and the tiled kernel (canonical) sum differently
+            assert torch.equal(outp, K.fp8_gemm(xq.to(cuda), xs.to(cuda), packed)), "not deterministic"
+            assert_gemm_close(outp, ref.fp8_gemm(xq, xs, wq, ws), f"packed M={M} N={N} K={Kd}")
 
 
 def test_pack_weight_layout(cuda):
@@ -162,7 +166,11 @@ def test_fp8_gemm_split_k_repeatable(cuda, M, N, Kd):
     xq, xs, wq, ws = xq.to(cuda), xs.to(cuda), wq.to(cuda), ws.to(cuda)
     packed = K.pack_weight(wq, ws)
     first = K.fp8_gemm(xq, xs, packed)
-    outs = [K.fp8_gemm(xq, xs, packed) for _ in range(30)] + [K.fp8_gemm(xq, xs, wq, ws) for _ in range(10)]
+    first_c = K.fp8_gemm(xq, xs, wq, ws)
+    outs = [K.fp8_gemm(xq, xs, packed) for _ in range(30)]
+    outs_c = [K.fp8_gemm(xq, xs, wq, ws) for _ in range(10)]
     torch.cuda.synchronize()
     for o in outs:
         assert torch.equal(o, first)
+    for o in outs_c:  # M > 64: another kernel for the canonical layout, also deterministic
+        assert torch.equal(o, first if M <= 64 else first_c)

@@ -588,8 +588,187 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
   if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- M > 64: MFMA GEMM
+// A workgroup of 4 waves computes a 128-row x 128-token output tile (one weight scale
+// block tall) over its K slice.  Per K block, both operands -- 8 packed weight fragments
+// and 8 fragments of the activation image, 2 KB of consecutive memory each -- plus the
+// block's 128 token scales and its weight scale are copied global -> LDS by the
+// load-to-LDS path (no registers, 10 copy instructions per wave), into a ring of S
+// stages: the copies of block i + S - 1 are issued while block i is computed.  Waves are
+// a 2 x 2 grid over the tile: each holds 4 row tiles x 4 token tiles of accumulators
+// (16 MFMAs per K block, 8 operand fragments read from LDS), so an LDS byte feeds 2
+// MFMAs and each global byte of the tile is fetched once per workgroup.
+constexpr int kMmStageBytes = 32768 + 512 + 256;  // weights, activations, token scales, weight scale
+constexpr int kMmOps = 10;                         // copy instructions per wave per stage
+
+// s_waitcnt immediate: vmcnt(n), no wait on the other counters
+__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+typedef __attribute__((address_space(3))) uint8_t* lds_u8_ptr;
+
+// Load-to-LDS copies written as inline assembly: lane l copies SIZE bytes from its own
+// global address to LDS at (wave-uniform) lds + l * SIZE.  Through the builtin, the
+// compiler cannot tell these LDS writes from the operand reads of another ring stage and
+// puts a wait for every copy in flight before each LDS read; as assembly they are
+// invisible to it, and the kernel's own s_waitcnt + s_barrier order them.
+__device__ inline void copy_to_lds16(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ inline void copy_to_lds4(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+template <int S>
+__global__ __launch_bounds__(256) void fp8_gemm_mm_kernel(
+    const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
+    uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
+  // One LDS array per ring stage: the compiler can then tell that the copies into one
+  // stage never alias the operand reads from another, and does not wait for the copies in
+  // flight before every LDS read (which it does for offsets into one array).
+  __shared__ __attribute__((aligned(16))) uint8_t stage0[kMmStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t stage1[kMmStageBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t stage2[S > 2 ? kMmStageBytes : 16];
+  const int KB = K >> 7, NT = N >> 4, MTT = (M + 15) >> 4;
+  const int nb = blockIdx.x, mg = blockIdx.y;
+  const int ks = blockIdx.z, ksplit = gridDim.z;
+  const int kb_begin = ks * kb_per_split;
+  const int kb_last = min(KB, kb_begin + kb_per_split) - 1;
+  const int n = kb_last - kb_begin + 1;  // >= 1 (the plan leaves no slice empty)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int wn = wave & 1, wm = wave >> 1;
+
+  // copies of K block kb into stage buffer buf; every wave issues kMmOps of them
+  auto stage = [&](auto b) -> uint8_t* {
+    constexpr int B_ = decltype(b)::value;
+    return B_ == 0 ? stage0 : (B_ == 1 ? stage1 : stage2);
+  };
+  auto issue = [&](int kb, uint8_t* st) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int f = 2 * wave + u;
+      const uint8_t* w = B + packed_fragment(8 * nb + f, kb, NT) + lane * 16;
+      const uint8_t* x = X + (static_cast<size_t>(kb) * MTT + min(8 * mg + f, MTT - 1)) * 2048 + lane * 16;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        copy_to_lds16(w + h * 1024, st + f * 2048 + h * 1024);
+        copy_to_lds16(x + h * 1024, st + 16384 + f * 2048 + h * 1024);
+      }
+    }
+    // token scales: waves 0/2 copy tokens 0..63 of the group, 1/3 tokens 64..127 (the same
+    // bytes twice); past the image's last token the index is clamped (never stored)
+    const int tok = min(128 * mg + 64 * (wave & 1) + lane, MTT * 16 - 1);
+    copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + 32768 + 256 * (wave & 1));
+    copy_to_lds4(Bs + static_cast<size_t>(nb) * KB + kb, st + 32768 + 512);
+  };
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const uint8_t* st) {
+    v8i wf[4], xf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + lane * 16);
+      const uint4 hi = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + 1024 + lane * 16);
+      wf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 lo = *reinterpret_cast<const uint4*>(st + 16384 + (4 * wm + j) * 2048 + lane * 16);
+      const uint4 hi = *reinterpret_cast<const uint4*>(st + 16384 + (4 * wm + j) * 2048 + 1024 + lane * 16);
+      xf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+    const float bs = *reinterpret_cast<const float*>(st + 32768 + 512);
+    float sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = reinterpret_cast<const float*>(st + 32768)[64 * wm + 16 * j + r] * bs;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] += mfma_16x16x128_fp8(wf[i], xf[j]) * sc[j];
+  };
+
+  // ring: copies run S - 1 blocks ahead; past the slice the last block is re-copied, so
+  // every wave always has the same number of copies in flight (a fixed wait count)
+  static_for<S - 1>([&](auto j) { issue(kb_begin + min(static_cast<int>(decltype(j)::value), n - 1), stage(j)); });
+  for (int i0 = 0; i0 < n; i0 += S) {
+    static_for<S>([&](auto jj) {
+      constexpr int J = decltype(jj)::value;
+      const int i = i0 + J;
+      if (i < n) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * kMmOps));  // block i's copies (this wave's) landed
+        asm volatile("s_barrier" ::: "memory");                   // ... and every wave's
+        // into the stage block i - 1 used, which every wave has finished
+        issue(kb_begin + min(i + S - 1, n - 1), stage(std::integral_constant<int, (J + S - 1) % S>{}));
+        compute(stage(std::integral_constant<int, J>{}));
+      }
+    });
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the workgroup ends
+
+  // lane holds rows 128 nb + 16 (4 wn + i) + 4 g + (0..3) of token 128 mg + 64 wm + 16 j + r
+  auto token = [&](int j) { return 128 * mg + 64 * wm + 16 * j + r; };
+  auto column = [&](int i) { return 128 * nb + 16 * (4 * wn + i) + 4 * g; };
+  if (ksplit == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(acc[i][j]));
+    return;
+  }
+  // split-K: fp32 partials (agent-scope stores), then the last slice of the tile sums
+  // them in slice order
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (token(j) < M) {
+        float* dst = partial + (static_cast<size_t>(ks) * M + token(j)) * N + column(i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) __hip_atomic_store(dst + e, acc[i][j][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ uint32_t last;
+  const int tile = mg * (N >> 7) + nb;
+  if (tid == 0) last = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == static_cast<uint32_t>(ksplit - 1);
+  __syncthreads();
+  if (!last) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (token(j) < M) {
+        v4f sum = {0.f, 0.f, 0.f, 0.f};
+        for (int q0 = 0; q0 < ksplit; q0 += 4) {  // 4 slices' loads in flight, added in order
+          v4f v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float* src = partial + (static_cast<size_t>(min(q0 + u, ksplit - 1)) * M + token(j)) * N + column(i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[u][e] = __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            if (q0 + u < ksplit) sum += v[u];
+        }
+        store_out(out, token(j), column(i), pack_bf16x4(sum));
+      }
+  if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct GemmPlan {
-  bool tiled;  // M > 64: fp8_gemm_tiled_kernel
+  bool mm;     // M > 64, packed weight: fp8_gemm_mm_kernel
+  bool tiled;  // M > 64, canonical weight: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
   int row_groups;  // grid.x: 16-row tiles (GEMV) or 128-row groups (tiled)
@@ -608,13 +787,25 @@ struct GemmPlan {
 // Tiled (M > 64; measured faster than the per-row-tile kernel from M = 128 on, slower at
 // M = 32 and 64): the smallest split giving >= 512 workgroups (2 per CU) with slices of
 // at least 8 K blocks.
-static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K) {
+static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
-  p.tiled = M > 64;
+  p.mm = M > 64 && packed && N % 128 == 0 && K % (kBlock * kGroup) == 0;
+  p.tiled = M > 64 && !p.mm;
   p.depth = 2;
   p.rt = 1;
   p.xf = false;
+  if (p.mm) {
+    // 128 x 128 tiles; split K until there is a workgroup for every CU
+    const int tiles = static_cast<int>((N / 128) * cdiv(M, 128));
+    int s = std::max(1, std::min(static_cast<int>(cdiv(256, tiles)), KB / 4));
+    p.row_groups = static_cast<int>(N / 128);
+    p.kb_per_split = static_cast<int>(cdiv(KB, s));
+    p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
+    p.waves = 4;
+    p.xf = true;
+    return p;
+  }
   if (p.tiled) {
     p.row_groups = static_cast<int>(cdiv(N / 16, kTiledWaves));
     int s = static_cast<int>(cdiv(512, p.row_groups));
@@ -668,11 +859,29 @@ static size_t image_offset(const GemmPlan& p, int64_t M, int64_t N) {
 template <bool PACKED>
 static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, const float* Bs,
                        const OutRoute& out, int M, int N, int K, void* workspace, hipStream_t st) {
-  const GemmPlan p = plan_gemm(M, N, K);
+  const GemmPlan p = plan_gemm(M, N, K, PACKED);
   uint32_t* counters = p.ksplit > 1 ? static_cast<uint32_t*>(workspace) : nullptr;
   float* partial = p.ksplit > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
   const dim3 grid(p.row_groups / p.rt, p.ksplit);
   const int per = p.kb_per_split;
+  // From M = 16 on the activations are first rearranged into the workspace (act_image_kernel).
+  const uint8_t* xa = A;
+  const float* xsa = As;
+  if (p.xf) {
+    uint8_t* img = static_cast<uint8_t*>(workspace) + image_offset(p, M, N);
+    const int64_t KB = K / kBlock, mtt = cdiv(M, 16);
+    float* img_s = reinterpret_cast<float*>(img + KB * mtt * 2048);
+    hipLaunchKernelGGL(act_image_kernel, dim3(static_cast<unsigned>(cdiv(KB * mtt * 128, 256))), dim3(256), 0, st,
+                       A, As, img, img_s, M, K);
+    xa = img;
+    xsa = img_s;
+  }
+  if (p.mm) {
+    constexpr int S = 2;
+    hipLaunchKernelGGL((fp8_gemm_mm_kernel<S>), dim3(p.row_groups, static_cast<unsigned>(cdiv(M, 128)), p.ksplit), dim3(256),
+                       0, st, xa, xsa, B, Bs, out, partial, counters, M, N, K, per);
+    return check_launch("fp8_gemm");
+  }
   if (p.tiled) {
     auto launch = [&](auto tt_tag) -> int {
       constexpr int TT = decltype(tt_tag)::value;
@@ -687,18 +896,6 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
     };
     if (M <= 128) return launch(std::integral_constant<int, 8>{});
     return launch(std::integral_constant<int, 16>{});
-  }
-  // GEMV.  M > 16 first rearranges the activations into the workspace (act_image_kernel).
-  const uint8_t* xa = A;
-  const float* xsa = As;
-  if (p.xf) {
-    uint8_t* img = static_cast<uint8_t*>(workspace) + image_offset(p, M, N);
-    const int64_t KB = K / kBlock, mtt = cdiv(M, 16);
-    float* img_s = reinterpret_cast<float*>(img + KB * mtt * 2048);
-    hipLaunchKernelGGL(act_image_kernel, dim3(static_cast<unsigned>(cdiv(KB * mtt * 128, 256))), dim3(256), 0, st,
-                       A, As, img, img_s, M, K);
-    xa = img;
-    xsa = img_s;
   }
   auto gemv = [&](auto mt, auto w, auto d, auto rt, auto xf) {
     hipLaunchKernelGGL((fp8_gemm_kernel<decltype(mt)::value, decltype(w)::value, PACKED, decltype(d)::value,
@@ -761,9 +958,12 @@ using namespace tl;
 
 extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock || M > 256) return 0;
-  const GemmPlan p = plan_gemm(M, N, K);
-  if (p.ksplit == 1 && !p.xf) return 0;
-  return image_offset(p, M, N) + (p.xf ? act_image_bytes(M, K) : 0);
+  size_t need = 0;
+  for (bool packed : {false, true}) {  // one size serves both weight layouts
+    const GemmPlan p = plan_gemm(M, N, K, packed);
+    if (p.ksplit > 1 || p.xf) need = std::max(need, image_offset(p, M, N) + (p.xf ? act_image_bytes(M, K) : 0));
+  }
+  return need;
 }
 
 extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
