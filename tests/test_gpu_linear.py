@@ -83,6 +83,9 @@ GEMM_CASES = [
     (24, 6144, 512),    # 2 row tiles, 2 token tiles
     (48, 7168, 1024),   # 2 row tiles, 4 token tiles
     (64, 12288, 512),   # 4 row tiles, 4 token tiles
+    # M > 64, packed: stream-K MFMA GEMM
+    (65, 128, 512),     # one tile of 4 K blocks over 4 workgroups: 4 partials
+    (192, 1024, 2048),  # 16 tiles x 16 blocks over 256 workgroups: 1-unit ranges, a half-full token group
 ]
 
 

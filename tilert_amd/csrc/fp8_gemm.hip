@@ -589,17 +589,29 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 }
 
 // ---------------------------------------------------------------- M > 64: MFMA GEMM
-// A workgroup of 4 waves computes a 128-row x 128-token output tile (one weight scale
-// block tall) over its K slice.  Per K block, both operands -- 8 packed weight fragments
-// and 8 fragments of the activation image, 2 KB of consecutive memory each -- plus the
-// block's 128 token scales and its weight scale are copied global -> LDS by the
-// load-to-LDS path (no registers, 10 copy instructions per wave), into a ring of S
-// stages: the copies of block i + S - 1 are issued while block i is computed.  Waves are
-// a 2 x 2 grid over the tile: each holds 4 row tiles x 4 token tiles of accumulators
-// (16 MFMAs per K block, 8 operand fragments read from LDS), so an LDS byte feeds 2
-// MFMAs and each global byte of the tile is fetched once per workgroup.
+// Output tiles are 128 weight rows (one scale block) x 128 tokens.  Per K block, both
+// operands -- 8 packed weight fragments and 8 fragments of the activation image, 2 KB of
+// consecutive memory each -- plus the block's 128 token scales and its weight scale are
+// copied global -> LDS by the load-to-LDS path (no registers), into a ring of S stages:
+// the copies of block i + S - 1 are issued while block i is computed.  The waves form a
+// 2 x (8 / TJ) grid over the tile: each holds 4 row tiles x TJ token tiles of
+// accumulators (4 TJ MFMAs per K block from 4 + TJ fragments read from LDS).
+//
+// Two schedules (SK):
+//  * at >= 256 tiles, one tile per workgroup: S = 2 stages (67 KB), 4 waves (TJ = 4), two
+//    workgroups per CU, so that one's copies overlap the other's MFMAs;
+//  * below that, "stream-K": the work -- tiles x K blocks, tile-major -- is cut into one
+//    equal contiguous range per CU (256 workgroups, S = 4 stages of 134 KB, 8 waves, TJ =
+//    2).  A range covers a few tile segments; a segment that is a whole tile is stored
+//    directly, others publish fp32 partials and the segment that completes a tile sums
+//    the tile's partials in K order (deterministic).
+// Measured (MI355X, up 7168 -> 18432 / down 18432 -> 7168): M = 256 81 / 91 us, M = 128
+// 73 / 81 us; the per-row-tile tiled kernel before it took 268 / 374 and 143 / ~180 us.
+// What bounds it now is latency, not a unit: the MFMA pipe is busy 17% of the time
+// (SQ_VALU_MFMA_BUSY_CYCLES), waves wait on memory counters ~40%, and each K block costs a
+// workgroup barrier.
 constexpr int kMmStageBytes = 32768 + 512 + 256;  // weights, activations, token scales, weight scale
-constexpr int kMmOps = 10;                         // copy instructions per wave per stage
+constexpr int kMmGrid = 256;  // stream-K: one workgroup per CU
 
 // s_waitcnt immediate: vmcnt(n), no wait on the other counters
 __host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
@@ -620,150 +632,203 @@ __device__ inline void copy_to_lds4(const void* src, uint8_t* lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
 }
 
-template <int S>
-__global__ __launch_bounds__(256) void fp8_gemm_mm_kernel(
+// Stream-K schedule: workgroup g owns work units [g U / G, (g+1) U / G).
+struct MmSched {
+  int64_t U;  // tiles * KB
+  int G;
+  __host__ __device__ int64_t start(int g) const { return static_cast<int64_t>(g) * U / G; }
+  __host__ __device__ int owner(int64_t u) const {  // the g whose range holds u
+    int g = static_cast<int>(u * G / U);
+    while (g + 1 < G && start(g + 1) <= u) ++g;
+    while (g > 0 && start(g) > u) --g;
+    return g;
+  }
+};
+
+// Workgroups: one per CU, but never more than units, so that no range is empty (the
+// segment numbering below counts consecutive workgroups).
+// At >= 256 tiles, one tile per workgroup (two workgroups fit per CU with the short ring,
+// measured faster than stream-K there: 75 vs 98 us at 256 x 18432 x 7168).
+__host__ inline int mm_grid(int64_t tiles, int64_t U) {
+  if (tiles >= kMmGrid) return static_cast<int>(tiles);
+  return static_cast<int>(std::min<int64_t>(kMmGrid, U));
+}
+
+// Partial slots per tile: a tile of KB units meets at most this many workgroup ranges.
+__host__ inline int mm_max_segments(int64_t U, int G, int KB) {
+  const int64_t per = U / G;  // shortest range
+  return static_cast<int>(per > 0 ? cdiv(KB, per) + 1 : KB);
+}
+
+template <int S, int TJ, bool SK>
+__global__ __launch_bounds__(16 / TJ * 64) void fp8_gemm_mm_kernel(
     const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
-    uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
-  // One LDS array per ring stage: the compiler can then tell that the copies into one
-  // stage never alias the operand reads from another, and does not wait for the copies in
-  // flight before every LDS read (which it does for offsets into one array).
+    uint32_t* __restrict__ counters, int M, int N, int K, int max_seg) {
+  // One LDS array per ring stage: the operand reads of one stage then provably never
+  // alias the copies into another.
   __shared__ __attribute__((aligned(16))) uint8_t stage0[kMmStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t stage1[kMmStageBytes];
   __shared__ __attribute__((aligned(16))) uint8_t stage2[S > 2 ? kMmStageBytes : 16];
+  __shared__ __attribute__((aligned(16))) uint8_t stage3[S > 3 ? kMmStageBytes : 16];
+  __shared__ uint32_t last_flag;
+  static_assert(S >= 2 && S <= 4, "ring depth");
   const int KB = K >> 7, NT = N >> 4, MTT = (M + 15) >> 4;
-  const int nb = blockIdx.x, mg = blockIdx.y;
-  const int ks = blockIdx.z, ksplit = gridDim.z;
-  const int kb_begin = ks * kb_per_split;
-  const int kb_last = min(KB, kb_begin + kb_per_split) - 1;
-  const int n = kb_last - kb_begin + 1;  // >= 1 (the plan leaves no slice empty)
+  const int NB = N >> 7;
+  const int tiles = NB * static_cast<int>((M + 127) >> 7);
+  const MmSched sched{static_cast<int64_t>(tiles) * KB, static_cast<int>(gridDim.x)};
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int wn = wave & 1, wm = wave >> 1;
+  constexpr int FPW = TJ / 2;               // weight (and activation) fragments each wave copies
+  constexpr int OPS = 4 * FPW + 2;          // copy instructions per wave per stage
+  const int wn = wave & 1, wm = wave >> 1;  // rows 64 wn.., tokens 16 TJ wm..
 
-  // copies of K block kb into stage buffer buf; every wave issues kMmOps of them
   auto stage = [&](auto b) -> uint8_t* {
     constexpr int B_ = decltype(b)::value;
-    return B_ == 0 ? stage0 : (B_ == 1 ? stage1 : stage2);
+    return B_ == 0 ? stage0 : (B_ == 1 ? stage1 : (B_ == 2 ? stage2 : stage3));
   };
-  auto issue = [&](int kb, uint8_t* st) {
+
+  const int64_t u_end = sched.start(blockIdx.x + 1);
+  for (int64_t u = sched.start(blockIdx.x); u < u_end;) {
+    const int tile = static_cast<int>(u / KB);
+    const int kb0 = static_cast<int>(u % KB);
+    const int n = static_cast<int>(min(static_cast<int64_t>(KB - kb0), u_end - u));
+    const int nb = tile % NB, mg = tile / NB;
+
+    // copies of K block kb of this tile into stage buffer st
+    auto issue = [&](int kb, uint8_t* st) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = 2 * wave + u;
-      const uint8_t* w = B + packed_fragment(8 * nb + f, kb, NT) + lane * 16;
-      const uint8_t* x = X + (static_cast<size_t>(kb) * MTT + min(8 * mg + f, MTT - 1)) * 2048 + lane * 16;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        copy_to_lds16(w + h * 1024, st + f * 2048 + h * 1024);
-        copy_to_lds16(x + h * 1024, st + 16384 + f * 2048 + h * 1024);
+      for (int u = 0; u < FPW; ++u) {
+        const int f = FPW * wave + u;  // weight and activation fragments f of this wave
+        const uint8_t* w = B + packed_fragment(8 * nb + f, kb, NT) + lane * 16;
+        const uint8_t* x = X + (static_cast<size_t>(kb) * MTT + min(8 * mg + f, MTT - 1)) * 2048 + lane * 16;
+        copy_to_lds16(w, st + f * 2048);
+        copy_to_lds16(w + 1024, st + f * 2048 + 1024);
+        copy_to_lds16(x, st + 16384 + f * 2048);
+        copy_to_lds16(x + 1024, st + 16384 + f * 2048 + 1024);
       }
-    }
-    // token scales: waves 0/2 copy tokens 0..63 of the group, 1/3 tokens 64..127 (the same
-    // bytes twice); past the image's last token the index is clamped (never stored)
-    const int tok = min(128 * mg + 64 * (wave & 1) + lane, MTT * 16 - 1);
-    copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + 32768 + 256 * (wave & 1));
-    copy_to_lds4(Bs + static_cast<size_t>(nb) * KB + kb, st + 32768 + 512);
-  };
+      // token scales: wave w copies tokens 64 (w & 1) .. +63 of the group (pairs of waves
+      // write the same bytes); past the image's last token the index is clamped (never stored)
+      const int tok = min(128 * mg + 64 * (wave & 1) + lane, MTT * 16 - 1);
+      copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + 32768 + 256 * (wave & 1));
+      copy_to_lds4(Bs + static_cast<size_t>(nb) * KB + kb, st + 32768 + 512);
+    };
 
-  v4f acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  auto compute = [&](const uint8_t* st) {
-    v8i wf[4], xf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 lo = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + lane * 16);
-      const uint4 hi = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + 1024 + lane * 16);
-      wf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint4 lo = *reinterpret_cast<const uint4*>(st + 16384 + (4 * wm + j) * 2048 + lane * 16);
-      const uint4 hi = *reinterpret_cast<const uint4*>(st + 16384 + (4 * wm + j) * 2048 + 1024 + lane * 16);
-      xf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-    const float bs = *reinterpret_cast<const float*>(st + 32768 + 512);
-    float sc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sc[j] = reinterpret_cast<const float*>(st + 32768)[64 * wm + 16 * j + r] * bs;
+    v4f acc[4][TJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] += mfma_16x16x128_fp8(wf[i], xf[j]) * sc[j];
-  };
+      for (int j = 0; j < TJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  // ring: copies run S - 1 blocks ahead; past the slice the last block is re-copied, so
-  // every wave always has the same number of copies in flight (a fixed wait count)
-  static_for<S - 1>([&](auto j) { issue(kb_begin + min(static_cast<int>(decltype(j)::value), n - 1), stage(j)); });
-  for (int i0 = 0; i0 < n; i0 += S) {
-    static_for<S>([&](auto jj) {
-      constexpr int J = decltype(jj)::value;
-      const int i = i0 + J;
-      if (i < n) {
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * kMmOps));  // block i's copies (this wave's) landed
-        asm volatile("s_barrier" ::: "memory");                   // ... and every wave's
-        // into the stage block i - 1 used, which every wave has finished
-        issue(kb_begin + min(i + S - 1, n - 1), stage(std::integral_constant<int, (J + S - 1) % S>{}));
-        compute(stage(std::integral_constant<int, J>{}));
+    auto compute = [&](const uint8_t* st) {
+      v8i wf[4], xf[TJ];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + lane * 16);
+        const uint4 hi = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + 1024 + lane * 16);
+        wf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
       }
-    });
-  }
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the workgroup ends
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) {
+        const uint4 lo = *reinterpret_cast<const uint4*>(st + 16384 + (TJ * wm + j) * 2048 + lane * 16);
+        const uint4 hi = *reinterpret_cast<const uint4*>(st + 16384 + (TJ * wm + j) * 2048 + 1024 + lane * 16);
+        xf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      }
+      const float bs = *reinterpret_cast<const float*>(st + 32768 + 512);
+      float sc[TJ];
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) sc[j] = reinterpret_cast<const float*>(st + 32768)[16 * TJ * wm + 16 * j + r] * bs;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] += mfma_16x16x128_fp8(wf[i], xf[j]) * sc[j];
+    };
 
-  // lane holds rows 128 nb + 16 (4 wn + i) + 4 g + (0..3) of token 128 mg + 64 wm + 16 j + r
-  auto token = [&](int j) { return 128 * mg + 64 * wm + 16 * j + r; };
-  auto column = [&](int i) { return 128 * nb + 16 * (4 * wn + i) + 4 * g; };
-  if (ksplit == 1) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(acc[i][j]));
-    return;
-  }
-  // split-K: fp32 partials (agent-scope stores), then the last slice of the tile sums
-  // them in slice order
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (token(j) < M) {
-        float* dst = partial + (static_cast<size_t>(ks) * M + token(j)) * N + column(i);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) __hip_atomic_store(dst + e, acc[i][j][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  __shared__ uint32_t last;
-  const int tile = mg * (N >> 7) + nb;
-  if (tid == 0) last = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == static_cast<uint32_t>(ksplit - 1);
-  __syncthreads();
-  if (!last) return;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (token(j) < M) {
-        v4f sum = {0.f, 0.f, 0.f, 0.f};
-        for (int q0 = 0; q0 < ksplit; q0 += 4) {  // 4 slices' loads in flight, added in order
-          v4f v[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const float* src = partial + (static_cast<size_t>(min(q0 + u, ksplit - 1)) * M + token(j)) * N + column(i);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[u][e] = __hip_atomic_load(src + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            if (q0 + u < ksplit) sum += v[u];
+    // ring: copies run S - 1 blocks ahead; past the segment the last block is re-copied,
+    // so every wave always has the same number of copies in flight (a fixed wait count)
+    __syncthreads();  // the previous segment's last reads of every stage are done
+    static_for<S - 1>([&](auto j) { issue(kb0 + min(static_cast<int>(decltype(j)::value), n - 1), stage(j)); });
+    for (int i0 = 0; i0 < n; i0 += S) {
+      static_for<S>([&](auto jj) {
+        constexpr int J = decltype(jj)::value;
+        const int i = i0 + J;
+        if (i < n) {
+          __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * OPS));  // block i's copies (this wave's) landed
+          asm volatile("s_barrier" ::: "memory");                   // ... and every wave's
+          // into the stage block i - 1 used, which every wave has finished
+          issue(kb0 + min(i + S - 1, n - 1), stage(std::integral_constant<int, (J + S - 1) % S>{}));
+          compute(stage(std::integral_constant<int, J>{}));
         }
-        store_out(out, token(j), column(i), pack_bf16x4(sum));
+      });
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the stages are reused
+    // lane holds rows 128 nb + 16 (4 wn + i) + 4 g + (0..3) of token 128 mg + 64 wm + 16 j + r
+    auto token = [&](int j) { return 128 * mg + 16 * TJ * wm + 16 * j + r; };
+    auto column = [&](int i) { return 128 * nb + 16 * (4 * wn + i) + 4 * g; };
+    if (!SK || n == KB) {  // the whole tile (always, without stream-K)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(acc[i][j]));
+    } else {
+      // segment seg of the tile: fp32 partial into slot (tile, seg), agent-scope stores
+      const int64_t tile_u0 = static_cast<int64_t>(tile) * KB;
+      const int first = sched.owner(tile_u0);
+      const int seg = static_cast<int>(blockIdx.x) - first;
+      const int nseg = sched.owner(tile_u0 + KB - 1) - first + 1;
+      float* slot = partial + (static_cast<size_t>(tile) * max_seg + seg) * 16384;
+      // slot layout: [row tile i8 0..7][token tile j8 0..7][v4f per lane]
+      auto slot_off = [&](float* base, int i, int j) {
+        return base + ((static_cast<size_t>(4 * wn + i) * 8 + (TJ * wm + j)) * 64 + lane) * 4;
+      };
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+          float* d = slot_off(slot, i, j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) __hip_atomic_store(d + e, acc[i][j][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0)
+        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    static_cast<uint32_t>(nseg - 1);
+      __syncthreads();
+      if (last_flag) {
+        v4f (&sum)[4][TJ] = acc;  // this segment's own partial is in its slot now
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j) sum[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < nseg; ++q) {  // segments in K order
+          float* src = partial + (static_cast<size_t>(tile) * max_seg + q) * 16384;
+          v4f v[4][TJ];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+              const float* s_ = slot_off(src, i, j);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[i][j][e] = __hip_atomic_load(s_ + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) sum[i][j] += v[i][j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < TJ; ++j)
+            if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(sum[i][j]));
+        if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-  if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    u += n;
+  }
 }
 
 struct GemmPlan {
@@ -795,14 +860,11 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   p.depth = 2;
   p.rt = 1;
   p.xf = false;
-  if (p.mm) {
-    // 128 x 128 tiles; split K until there is a workgroup for every CU
-    const int tiles = static_cast<int>((N / 128) * cdiv(M, 128));
-    int s = std::max(1, std::min(static_cast<int>(cdiv(256, tiles)), KB / 4));
-    p.row_groups = static_cast<int>(N / 128);
-    p.kb_per_split = static_cast<int>(cdiv(KB, s));
-    p.ksplit = static_cast<int>(cdiv(KB, p.kb_per_split));
-    p.waves = 4;
+  if (p.mm) {  // stream-K over 128 x 128 tiles, one workgroup per CU
+    p.row_groups = kMmGrid;
+    p.ksplit = 1;
+    p.kb_per_split = KB;
+    p.waves = 8;
     p.xf = true;
     return p;
   }
@@ -851,8 +913,16 @@ constexpr int kMaxRowTiles = 16384;  // N <= 262144
 constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 
 // Workspace: counters, then the split-K partials, then the activation image (256-aligned).
-static size_t image_offset(const GemmPlan& p, int64_t M, int64_t N) {
-  const size_t partial = p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0;
+static size_t mm_partial_bytes(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = (N / 128) * cdiv(M, 128), KB = K / kBlock;
+  const int G = mm_grid(tiles, tiles * KB);
+  if (G == tiles) return 0;  // a whole tile per workgroup: no partials
+  return static_cast<size_t>(tiles) * mm_max_segments(tiles * KB, G, static_cast<int>(KB)) * 16384 * sizeof(float);
+}
+
+static size_t image_offset(const GemmPlan& p, int64_t M, int64_t N, int64_t K) {
+  const size_t partial = p.mm ? mm_partial_bytes(M, N, K)
+                              : (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0);
   return kCounterBytes + (partial + 255) / 256 * 256;
 }
 
@@ -868,7 +938,7 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
   const uint8_t* xa = A;
   const float* xsa = As;
   if (p.xf) {
-    uint8_t* img = static_cast<uint8_t*>(workspace) + image_offset(p, M, N);
+    uint8_t* img = static_cast<uint8_t*>(workspace) + image_offset(p, M, N, K);
     const int64_t KB = K / kBlock, mtt = cdiv(M, 16);
     float* img_s = reinterpret_cast<float*>(img + KB * mtt * 2048);
     hipLaunchKernelGGL(act_image_kernel, dim3(static_cast<unsigned>(cdiv(KB * mtt * 128, 256))), dim3(256), 0, st,
@@ -877,9 +947,18 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
     xsa = img_s;
   }
   if (p.mm) {
-    constexpr int S = 2;
-    hipLaunchKernelGGL((fp8_gemm_mm_kernel<S>), dim3(p.row_groups, static_cast<unsigned>(cdiv(M, 128)), p.ksplit), dim3(256),
-                       0, st, xa, xsa, B, Bs, out, partial, counters, M, N, K, per);
+    uint32_t* cnt = static_cast<uint32_t*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    const int64_t tiles = (N / 128) * cdiv(M, 128), U = tiles * (K / kBlock);
+    const int G = mm_grid(tiles, U);
+    const int max_seg = mm_max_segments(U, G, K / kBlock);
+    if (G == tiles) {  // a whole tile per workgroup, 2 workgroups per CU: 2-stage ring of 67 KB, 4 waves
+      hipLaunchKernelGGL((fp8_gemm_mm_kernel<2, 4, false>), dim3(G), dim3(4 * 64), 0, st, xa, xsa, B, Bs, out, part, cnt, M, N,
+                         K, max_seg);
+    } else {  // stream-K, 1 workgroup per CU: 4-stage ring of 134 KB, 8 waves
+      hipLaunchKernelGGL((fp8_gemm_mm_kernel<4, 2, true>), dim3(G), dim3(8 * 64), 0, st, xa, xsa, B, Bs, out, part, cnt, M, N,
+                         K, max_seg);
+    }
     return check_launch("fp8_gemm");
   }
   if (p.tiled) {
@@ -961,7 +1040,7 @@ extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   size_t need = 0;
   for (bool packed : {false, true}) {  // one size serves both weight layouts
     const GemmPlan p = plan_gemm(M, N, K, packed);
-    if (p.ksplit > 1 || p.xf) need = std::max(need, image_offset(p, M, N) + (p.xf ? act_image_bytes(M, K) : 0));
+    if (p.ksplit > 1 || p.xf || p.mm) need = std::max(need, image_offset(p, M, N, K) + (p.xf ? act_image_bytes(M, K) : 0));
   }
   return need;
 }
