@@ -326,7 +326,7 @@ def main() -> int:
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("fp8_gemm_M4_7168x18432.md"),
                      "traffic_source": "profiles/fp8_gemm_M4_7168x18432.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
-                     "kernel": "tl::fp8_gemm_kernel<1, 8, true>", "bytes_per_call": nbytes},
+                     "kernel": "tl::fp8_gemm_kernel<1, 8, true, 4, 1, false>", "bytes_per_call": nbytes},
     }
     if not args.no_cpu_baseline:
         q, s, _ = ws[0]
