@@ -26,6 +26,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+WARMUP_MIN_S = 0.2
 METRIC = "µs/call + achieved HBM GB/s (% of peak) for FP8 block-scaled GEMM at M=4"
 
 
@@ -38,9 +39,15 @@ def _graph_time_us(torch, fn, steps: int, warmup: int) -> float:
     with torch.cuda.graph(g):
         for i in range(steps):
             fn(i)
-    for _ in range(max(1, warmup // max(1, steps) + 1)):
+    # Untimed warm-up: at least `warmup` calls and at least WARMUP_MIN_S of replays, so the
+    # GPU clocks have ramped before the timed replay (one replay alone left per-call times
+    # varying by +-0.5 us between otherwise identical runs).
+    t_end = time.perf_counter() + WARMUP_MIN_S
+    done = 0
+    while done < max(1, warmup) or time.perf_counter() < t_end:
         g.replay()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        done += steps
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -321,7 +328,8 @@ def main() -> int:
         "data": "synthetic (seeded randn weights N(0,0.02) block-quantised 128x128; x N(0,1) act_quant 1x128)",
         "config": {"workload": "fp8_block_scaled_linear_7168x18432_M4", "M": M, "K": Kd, "N": N,
                    "weight_layout": "mfma-fragment-packed", "weight_copies_rotated": 5,
-                   "timing": "HIP graph of K calls, HIP events around the replay"},
+                   "timing": "HIP graph of K calls, HIP events around the replay",
+                   "warmup_policy": f"max(W calls, {WARMUP_MIN_S} s of untimed replays)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic("fp8_gemm_M4_7168x18432.md"),
