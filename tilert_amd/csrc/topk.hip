@@ -2,10 +2,11 @@
 // is torch.topk, :128-143), as ONE kernel with one cross-workgroup barrier and one handoff.
 //
 // Scores map to order-preserving 32-bit keys (larger score = larger key).  A row is cut
-// into chunks of 256 * PT columns, one 256-thread workgroup each (PT contiguous columns
-// per thread, kept in registers).  Small workgroups keep the LDS histogram's atomic
-// traffic per CU low: keys bunch into a few bins (sign, exponent and two mantissa bits),
-// and same-bin LDS atomics serialise.
+// into chunks of 1024 * PT columns, one 1024-thread workgroup each (PT contiguous columns
+// per thread, kept in registers).  Sixteen waves per workgroup hide the LDS and memory
+// latencies that dominate the one-workgroup final stage (measured: a 256-thread
+// workgroup with 32 candidates per thread spent ~1.5 us on each radix pass and on the
+// emission, nearly all of it waiting).
 //   Stage 1 (every chunk): a histogram of the keys' top 11 bits in LDS; its non-zero bins
 //     are added into its group's copy of the row histogram with agent-scope atomics.  The
 //     row's last chunk to arrive (two-level counter) sums the copies, finds the digit d0
@@ -21,12 +22,12 @@
 //     8192 and stay in registers when one batch holds them; otherwise every pass streams
 //     the batches again, so any input is exact.  The last chunk re-arms the counters.
 // Scans use DPP row shifts and row broadcasts inside a wave (no LDS round trips) and one
-// LDS exchange across the four waves.
+// LDS exchange across the sixteen waves.
 // The set is exact and deterministic, ties included.  Measured on MI355X, the cost is a
 // chain of device-scope round trips (~0.25 us each when uncontended; same-address atomics
 // serialise at tens of ns each, hence the groups), not bandwidth.
 //
-// The barrier needs a launch's workgroups co-resident: a launch holds at most 256
+// The barrier needs a launch's workgroups co-resident: a launch holds at most 128
 // workgroups (larger inputs are launched in groups of rows), and the wait is bounded
 // (about a second) so a wave can never hang.
 //
@@ -40,23 +41,25 @@
 
 namespace tl {
 
-constexpr int kTkThreads = 256;
+constexpr int kTkThreads = 1024;
 constexpr int kTkWaves = kTkThreads / 64;
 constexpr int kBins = 2048;                           // widest digit: 11 bits
-constexpr int kBinsPerThread = kBins / kTkThreads;    // 8
+constexpr int kBinsPerThread = kBins / kTkThreads;    // 2
+static_assert(kBinsPerThread == 2, "the histogram code below moves 2 bins per thread");
 constexpr int kMaxK = 8192;
 constexpr int kMaxCols = 262144;
-constexpr int kMaxGroups = 256;                       // workgroups per launch
+constexpr int kMaxGroups = 128;                       // workgroups per launch (one per CU, half the chip)
 constexpr int kMaxChunks = 256;                       // per row
-constexpr int kCandPerThread = 32;                    // stage-2 register batch per thread
+constexpr int kCandPerThread = 8;                     // stage-2 register batch per thread
 constexpr int kCandBatch = kTkThreads * kCandPerThread;
 constexpr uint32_t kSpinLimit = 1u << 22;             // x s_sleep(8): ~1 s
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2t __attribute__((ext_vector_type(2)));
 
 // The workspace starts with a fixed state region -- per launch slot (blockIdx.y, at most
-// 256 rows per launch): arrival counters, the broadcast word and the row histograms --
+// 128 rows per launch): arrival counters, the broadcast word and the row histograms --
 // that must be zero when a call starts and is left zero by every call.  Its offsets do
 // not depend on the problem shape, so calls of any shapes can share one workspace without
 // one call's candidates landing on another call's state.
@@ -136,13 +139,13 @@ __device__ inline uint32_t wave_incl_scan(uint32_t x) {
 }
 
 struct TopkShared {
-  uint32_t h[kBins];
+  uint32_t h[kBins + 64];  // + one spare bin per lane (branch-free histogram adds)
   uint32_t waves[2][kTkWaves];
   uint32_t digit, above, dcount, flag;
   uint32_t offs[kMaxChunks + 1];
 };
 
-// Block-wide exclusive prefix sum over the 256 threads (and the block total).  The two
+// Block-wide exclusive prefix sum over the 1024 threads (and the block total).  The two
 // wave-total slots alternate between calls, so one barrier per scan suffices: a slot is
 // rewritten only after the next scan's barrier, which every reader of it has passed.
 __device__ inline uint32_t block_excl_scan(uint32_t v, TopkShared& sh, int& slot, uint32_t& total) {
@@ -206,11 +209,8 @@ __device__ inline bool arrive_last(uint32_t* level1, uint32_t* level2, int chunk
   return p2 == static_cast<uint32_t>(groups - 1);
 }
 
-__device__ inline void zero_bins(TopkShared& sh) {  // thread t clears bins 8t .. 8t+7
-  u32x4t* h4 = reinterpret_cast<u32x4t*>(sh.h) + threadIdx.x * 2;
-  const u32x4t z = {0u, 0u, 0u, 0u};
-  h4[0] = z;
-  h4[1] = z;
+__device__ inline void zero_bins(TopkShared& sh) {  // thread t clears bins 2t, 2t+1
+  reinterpret_cast<u32x2t*>(sh.h)[threadIdx.x] = u32x2t{0u, 0u};
 }
 
 template <int PT>
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
   constexpr int kChunk = kTkThreads * PT;
   static_assert(PT % 4 == 0 && PT <= 32, "float4 loads, one mask bit per key");
   __shared__ TopkShared sh;
-  extern __shared__ uint64_t stage[];  // [kCandBatch / 32 * 33]: the stage-2 batch staging buffer
+  extern __shared__ uint64_t stage[];  // [kCandBatch / kCandPerThread * (kCandPerThread + 1)]: stage-2 staging
   int slot = 0;
   const int row = row0 + static_cast<int>(blockIdx.y), y = blockIdx.y;
   const int chunks = gridDim.x, chunk = blockIdx.x;
@@ -260,57 +260,49 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
   for (int i = 0; i < PT; ++i)
     if ((vm >> i) & 1u) atomicAdd(&sh.h[key[i] >> 21], 1u);
   __syncthreads();
-  // this chunk's non-zero bins into its group's histogram (thread t: bins 8t .. 8t+7)
+  // this chunk's non-zero bins into its group's histogram (thread t: bins 2t, 2t+1)
   const int groups = min(kGroups, chunks), grp = chunk % groups;
   uint32_t* rh = ws.hist + static_cast<int64_t>(y) * chunks * kBins;  // group g's at rh + g*kBins
   {
-    const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h) + threadIdx.x * 2;
-    const u32x4t a = h4[0], b = h4[1];
-    const uint32_t hv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    const u32x2t a = reinterpret_cast<const u32x2t*>(sh.h)[threadIdx.x];
+    const uint32_t hv[2] = {a.x, a.y};
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 2; ++i)
       if (hv[i])
-        __hip_atomic_fetch_add(&rh[grp * kBins + threadIdx.x * 8 + i], hv[i], __ATOMIC_RELAXED,
+        __hip_atomic_fetch_add(&rh[grp * kBins + threadIdx.x * 2 + i], hv[i], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) sh.flag = arrive_last(ws.arrive1 + y * kGroups, ws.arrive2 + y, chunk, chunks, groups);
   __syncthreads();
-  // The row's last chunk to arrive sums the group histograms (thread t: digits hi-1 ..
-  // hi-8, hi = 2048 - 8t), finds d0, broadcasts (valid bit, d0, above0) and re-zeroes the
+  // The row's last chunk to arrive sums the group histograms (thread t: digits hi-1,
+  // hi-2, hi = 2048 - 2t), finds d0, broadcasts (valid bit, d0, above0) and re-zeroes the
   // histograms; the others wait for their group's replica of that word (bounded spin).
   if (sh.flag) {
     const uint32_t hi = kBins - threadIdx.x * kBinsPerThread;
-    // 16-byte loads that bypass the non-coherent cache level (sc1), as the agent-scope
+    // 8-byte loads that bypass the non-coherent cache level (sc1), as the agent-scope
     // atomic loads do; every sub-histogram's atomics completed before its chunk arrived
     const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(rh, 0, kGroups * kBins * 4, kBufferRsrcWord3);
-    u32x4t a[kGroups], b[kGroups];
+    u32x2t a[kGroups];
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) {
-      const int off = (g < groups ? g : 0) * kBins * 4 + static_cast<int>(hi - 8) * 4;
-      a[g] = __builtin_amdgcn_raw_buffer_load_b128(hr, off, 0, kCachePolicySc1);
-      b[g] = __builtin_amdgcn_raw_buffer_load_b128(hr, off + 16, 0, kCachePolicySc1);
+      const int off = (g < groups ? g : 0) * kBins * 4 + static_cast<int>(hi - 2) * 4;
+      a[g] = __builtin_bit_cast(u32x2t, __builtin_amdgcn_raw_buffer_load_b64(hr, off, 0, kCachePolicySc1));
     }
     uint32_t cnt[kBinsPerThread] = {};
 #pragma unroll
     for (int g = 0; g < kGroups; ++g) {
       if (g < groups) {
-        const uint32_t v[8] = {b[g].w, b[g].z, b[g].y, b[g].x, a[g].w, a[g].z, a[g].y, a[g].x};
-#pragma unroll
-        for (int i = 0; i < kBinsPerThread; ++i) cnt[i] += v[i];
+        cnt[0] += a[g].y;
+        cnt[1] += a[g].x;
       }
     }
     uint32_t d, above, dc;
     pick_digit(cnt, hi, static_cast<uint32_t>(k), sh, slot, d, above, dc);
     if (threadIdx.x < static_cast<unsigned>(groups)) st_agent(&ws.bcast[y * kGroups + threadIdx.x], 0x80000000u | (d << 13) | above);
     // re-zeroed after the broadcast: nothing reads them again before this kernel ends
-    const u32x4t z = {0u, 0u, 0u, 0u};
-    for (int g = 0; g < groups; ++g) {
-      u32x4t* p4 = reinterpret_cast<u32x4t*>(rh + g * kBins + hi - 8);
-      p4[0] = z;
-      p4[1] = z;
-    }
+    for (int g = 0; g < groups; ++g) *reinterpret_cast<u32x2t*>(rh + g * kBins + hi - 2) = u32x2t{0u, 0u};
   } else if (threadIdx.x == 0) {
     uint32_t w = 0;
     for (uint32_t it = 0; it < kSpinLimit; ++it) {
@@ -346,24 +338,27 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
 
   // ---- stage 2 (the row's last chunk)
   const uint64_t* rc = ws.cand + static_cast<int64_t>(row) * chunks * kChunk;
+  const __amdgpu_buffer_rsrc_t crs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(rc), 0,
+                                                                       chunks * kChunk * 8, kBufferRsrcWord3);
   // offsets of every chunk's candidates (entries past the last chunk hold C)
   uint32_t C;
   {
     const uint32_t cn = threadIdx.x < static_cast<unsigned>(chunks)
                             ? ld_agent(&ws.count[static_cast<int64_t>(row) * chunks + threadIdx.x]) : 0u;
-    sh.offs[threadIdx.x] = block_excl_scan(cn, sh, slot, C);
+    const uint32_t before = block_excl_scan(cn, sh, slot, C);
+    if (threadIdx.x < static_cast<unsigned>(kMaxChunks)) sh.offs[threadIdx.x] = before;
     if (threadIdx.x == 0) sh.offs[kMaxChunks] = C;
     __syncthreads();
   }
   int lg = 0;  // binary-search depth: smallest power of two >= chunks
   while ((1 << lg) < chunks) ++lg;
-  // CPT candidates per thread: 16 when the candidates fit one batch of 4096 (the common
-  // case, fewer registers and instructions), else 32 (batches of 8192).
+  // CPT candidates per thread: 4 when the candidates fit one batch of 4096 (the common
+  // case, fewer registers and instructions), else 8 (batches of 8192).
   auto select = [&](auto cpt_tag) __attribute__((always_inline)) {
     constexpr int CPT = decltype(cpt_tag)::value;
     constexpr int CB = kTkThreads * CPT;
-    // Candidate batches of CB = 256 * CPT in column order.  A batch is read coalesced
-    // (thread t loads j = b0 + 256 i + t), staged in LDS, and taken back as CPT contiguous
+    // Candidate batches of CB = 1024 * CPT in column order.  A batch is read coalesced
+    // (thread t loads j = b0 + 1024 i + t), staged in LDS, and taken back as CPT contiguous
     // candidates per thread (j = b0 + CPT t + i), so thread order is column order.  Rows
     // padded to CPT + 1 entries keep both LDS access patterns free of bank conflicts.
     uint64_t cv[CPT];
@@ -384,11 +379,18 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
           c[i] = sh.offs[nc] <= j[i] ? nc : c[i];
         }
       }
+      // all offsets first, then the candidate loads: plain sc1 buffer loads (past this
+      // XCD's L2, like the agent-scope atomic loads) that the compiler can keep in flight
+      // together -- atomic loads interleaved with the LDS reads waited on each read
+      uint32_t off[CPT];
+  #pragma unroll
+      for (int i = 0; i < CPT; ++i) off[i] = sh.offs[c[i]];
       uint64_t v[CPT];
   #pragma unroll
-      for (int i = 0; i < CPT; ++i)
-        v[i] = __hip_atomic_load(rc + static_cast<int64_t>(c[i]) * kChunk + (j[i] - sh.offs[c[i]]), __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < CPT; ++i) {
+        const uint32_t e = static_cast<uint32_t>(c[i]) * kChunk + (j[i] - off[i]);
+        v[i] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(crs, static_cast<int>(e * 8u), 0, kCachePolicySc1));
+      }
       __syncthreads();  // the previous batch's staging reads are complete
   #pragma unroll
       for (int i = 0; i < CPT; ++i) {
@@ -427,25 +429,28 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
       zero_bins(sh);
       __syncthreads();
       for_batches([&](uint32_t m) __attribute__((always_inline)) {
+        // a slot is skipped when no lane of the wave has a match (wave-uniform test);
+        // otherwise lanes without one add into their own spare bin (no branch, no
+        // same-address conflict)
+        const uint32_t spare = kBins + (threadIdx.x & 63);
   #pragma unroll
         for (int i = 0; i < CPT; ++i) {
           const uint32_t kk = static_cast<uint32_t>(cv[i] >> 32);
-          if (((m >> i) & 1u) && (kk >> (shift + width)) == prefix)
-            atomicAdd(&sh.h[(kk >> shift) & ((1u << width) - 1u)], 1u);
+          const bool hit = ((m >> i) & 1u) && (kk >> (shift + width)) == prefix;
+          if (__builtin_amdgcn_ballot_w64(hit))
+            atomicAdd(&sh.h[hit ? (kk >> shift) & ((1u << width) - 1u) : spare], 1u);
         }
       });
       __syncthreads();
       uint32_t d, above, dc;
-      if (pass == 1) {  // 2048 digits, 8 per thread
-        const uint32_t hi = kBins - threadIdx.x * 8;
-        const u32x4t* h4 = reinterpret_cast<const u32x4t*>(sh.h + hi - 8);
-        const u32x4t a = h4[0], b = h4[1];
-        const uint32_t cnt[8] = {b.w, b.z, b.y, b.x, a.w, a.z, a.y, a.x};
+      if (pass == 1) {  // 2048 digits, 2 per thread
+        const uint32_t hi = kBins - threadIdx.x * 2;
+        const u32x2t a = *reinterpret_cast<const u32x2t*>(sh.h + hi - 2);
+        const uint32_t cnt[2] = {a.y, a.x};
         pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
-      } else {  // 1024 digits, 4 per thread
-        const uint32_t hi = (kBins / 2) - threadIdx.x * 4;
-        const u32x4t a = *reinterpret_cast<const u32x4t*>(sh.h + hi - 4);
-        const uint32_t cnt[4] = {a.w, a.z, a.y, a.x};
+      } else {  // 1024 digits, 1 per thread
+        const uint32_t hi = (kBins / 2) - threadIdx.x;
+        const uint32_t cnt[1] = {sh.h[hi - 1]};
         pick_digit(cnt, hi, k_rem, sh, slot, d, above, dc);
       }
       prefix = (prefix << width) | d;
@@ -459,6 +464,24 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
     // emit: candidates above T, then those equal to T (compared on bits >= tshift) in
     // column order until need_eq, all in ascending column order
     uint32_t base = 0, eq_base = 0;
+    if (resolved) {  // every key of the threshold bin is taken: one scan per batch
+      for_batches([&](uint32_t m) __attribute__((always_inline)) {
+        uint32_t sel = 0;
+  #pragma unroll
+        for (int i = 0; i < CPT; ++i)
+          sel |= (((m >> i) & 1u) && (static_cast<uint32_t>(cv[i] >> 32) >> tshift) >= T) ? (1u << i) : 0u;
+        uint32_t sel_tot;
+        uint32_t p = base + block_excl_scan(__builtin_popcount(sel), sh, slot, sel_tot);
+  #pragma unroll
+        for (int i = 0; i < CPT; ++i)
+          if ((sel >> i) & 1u) {
+            if (p < static_cast<uint32_t>(k)) o[p] = static_cast<int32_t>(static_cast<uint32_t>(cv[i]));
+            ++p;
+          }
+        base += sel_tot;
+      });
+      return;
+    }
     for_batches([&](uint32_t m) __attribute__((always_inline)) {
       uint32_t n_eq = 0;
   #pragma unroll
@@ -487,10 +510,10 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
       eq_base += eq_tot;
     });
   };
-  if (C <= static_cast<uint32_t>(kTkThreads * 16))
-    select(std::integral_constant<int, 16>{});
+  if (C <= static_cast<uint32_t>(kTkThreads * 4))
+    select(std::integral_constant<int, 4>{});
   else
-    select(std::integral_constant<int, 32>{});
+    select(std::integral_constant<int, 8>{});
 
   // every chunk is past the broadcast and has published its candidates: re-arm the row's
   // counters (last, so that no wait on these stores delays the selection)
@@ -511,18 +534,17 @@ using namespace tl;
 
 namespace {
 
-// Columns per thread: 16 when every row of the call fits one launch that way (rows *
-// chunks <= 256; measured faster than 8 per thread at 4 x 128K), otherwise 32, and rows
-// are launched in groups.
+// Columns per thread: 4 (chunks of 4096) when every row of the call fits one launch that
+// way (rows * chunks <= 256), otherwise 8, and rows are launched in groups.
 struct TopkPlan {
   int pt, chunks, rows_per_launch;
 };
 
 TopkPlan plan_topk(int64_t rows, int64_t ld) {
-  TopkPlan p{32, 0, 0};
-  for (int pt : {16, 32}) {
+  TopkPlan p{8, 0, 0};
+  for (int pt : {4, 8}) {
     const int64_t ch = cdiv(ld, static_cast<int64_t>(kTkThreads) * pt);
-    if (rows * ch <= kMaxGroups || pt == 32) {
+    if (rows * ch <= kMaxGroups || pt == 8) {
       p.pt = pt;
       p.chunks = static_cast<int>(ch);
       break;
@@ -560,8 +582,8 @@ extern "C" int tl_topk_rows(const float* logits, int64_t rows, int64_t ld, int64
     return kErrUnsupported;
   }
   const TopkWs ws = carve(workspace, rows, p.chunks);
-  auto kern = p.pt == 16 ? topk_kernel<16> : topk_kernel<32>;
-  const int stage_bytes = kCandBatch / 32 * 33 * static_cast<int>(sizeof(uint64_t));
+  auto kern = p.pt == 4 ? topk_kernel<4> : topk_kernel<8>;
+  const int stage_bytes = kCandBatch / kCandPerThread * (kCandPerThread + 1) * static_cast<int>(sizeof(uint64_t));
   if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(kern), stage_bytes, "topk"))
     return rc;
   for (int64_t r0 = 0; r0 < rows; r0 += p.rows_per_launch) {
