@@ -130,6 +130,25 @@ __device__ inline float load_f32_vector(const float* p) {
   return p[zero];
 }
 
+// s_waitcnt immediate: vmcnt(n), no wait on the other counters
+__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+typedef __attribute__((address_space(3))) uint8_t* lds_u8_ptr;
+
+// Load-to-LDS copies written as inline assembly: lane l copies SIZE bytes from its own
+// global address to LDS at (wave-uniform) lds + l * SIZE.  Through the builtin, the
+// compiler cannot tell these LDS writes from the operand reads of another ring stage and
+// puts a wait for every copy in flight before each LDS read; as assembly they are
+// invisible to it, and the kernel's own s_waitcnt + s_barrier order them.
+__device__ inline void copy_to_lds16(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ inline void copy_to_lds4(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
 // Software pipeline over n items with D operand buffers: item i's loads are issued D-1
 // items ahead of its compute.  fetch(i, buf) must issue the same, unconditional loads for
 // every i, so the steady-state loop has a fixed number of loads in flight and the
