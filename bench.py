@@ -13,7 +13,7 @@ repeat reads.
 
 ``--extras`` adds (outside the JSON contract's required keys, under "extras") the MLA
 projections (config 1), the MoE layer (config 2), the M sweep (config 3) and the
-indexer + top-k at 128K (config 4).
+indexer + top-k at 128K (config 4), and the indexer key producer.
 """
 from __future__ import annotations
 
@@ -273,6 +273,25 @@ def extras(torch, steps, dev):
     us_p = _graph_time_us(torch, lambda i: si.sparse_index_paged(q, qsc, pages[i % 20], w, logits, L - 4, L), st, 5)
     out["indexer_paged_128k_M4"] = {"scores_us": round(us_p, 2), "scores_GBs": round(b_s / us_p / 1e3, 1),
                                     "scores_hbm_frac": round(b_s / us_p / 1e3 / HBM_PEAK_GBS, 3)}
+    del pages
+
+    # the indexer key producer at decode (M = 4 new keys): LayerNorm -> RoPE -> Hadamard into
+    # the KI pages in one launch, against the bf16 cache write followed by the page writer
+    from tilert_amd.layernorm_rope_rotate import layernorm_rope_rotate, layernorm_rope_rotate_ki
+    kx = torch.randn(1, M, 128, device=dev).to(torch.bfloat16)
+    kw, kb = torch.ones(128, device=dev), torch.zeros(128, device=dev)
+    th = torch.rand(M, 32, device=dev) * 6.28
+    kf = torch.stack([th.cos(), th.sin()], -1).reshape(M, 1, 64).contiguous()
+    kpos = torch.tensor([L - 4], dtype=torch.int32, device=dev)
+    kpages = torch.zeros(L // 64, si.KI_PAGE_BYTES, dtype=torch.uint8, device=dev)
+    kcache = torch.zeros(1, L, 128, dtype=torch.bfloat16, device=dev)
+    us_f = _graph_time_us(torch, lambda i: layernorm_rope_rotate_ki(kx, kpos, kpages, kw, kb, kf), st, 5)
+
+    def two_step(i):
+        layernorm_rope_rotate(kx, kpos, kcache, kw, kb, kf, None, "deepseek_v3_2")
+        si.ki_cache_write(kcache[0, L - 4:], kpages, L - 4)
+    us_2 = _graph_time_us(torch, two_step, st, 5)
+    out["ki_producer_M4"] = {"fused_us": round(us_f, 2), "bf16_cache_then_page_write_us": round(us_2, 2)}
     return out
 
 

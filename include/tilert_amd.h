@@ -27,6 +27,10 @@
  *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
  *   tl_indexer_fp8_scores_paged  the same over KI pages    pd_vllm/profiles/mla_nsa.py:211-228
  *   tl_ki_cache_write      writer of the KI page format    pd_vllm/profiles/mla_nsa.py:17-41
+ *   tl_layernorm_rope_rotate     layernorm_rope_rotate_op  .../ops/layernorm_rope_rotate.py:23-82
+ *                                (golden :206-220)
+ *   tl_layernorm_rope_rotate_ki  the same, its keys quantised into KI pages (the producer of
+ *                                the format tl_indexer_fp8_scores_paged reads)
  *   tl_topk_rows           topk_accurate_op               .../ops/topk.py:62-109
  *   (sparse_index_topk_dsv32_op, .../ops/sparse_index.py:72-128, = scores + top-k)
  */
@@ -196,6 +200,27 @@ int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per
  * (ops/layernorm_rope_rotate.py:206-220) happens upstream.  pos + rows <= 64 * n_pages. */
 int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t n_pages, int64_t pos,
                       int scale_mode, void* stream);
+
+/* Indexer key producer, LayerNormRoPERotate (ops/layernorm_rope_rotate.py:23-82, golden
+ * :206-220): for each of `seq` bf16 keys x [seq, 128], k = bf16(LayerNorm(x) * weight +
+ * bias) with fp32 statistics and the given eps (the golden's 1e-6); dims 0..63 take the
+ * non-interleaved RoPE (element i pairs with i + 32, times the complex freqs[t, i]; freqs is
+ * fp32 [seq, 64] = (cos, sin) interleaved, the op's view_as_real of freqs_cis), rounded to
+ * bf16; then the 128-point Hadamard transform scaled by 128^-1/2 (rotate_activation,
+ * ops/rotate.py:17-21), rounded to bf16.  weight, bias fp32 [128].  Key t is written to row
+ * *cur_pos + t (cur_pos: device int32) of k_cache_bf16 [cache_rows, 128]; rows outside the
+ * cache are dropped.  Replaces layernorm_rope_rotate_op. */
+int tl_layernorm_rope_rotate(const void* x_bf16, int64_t seq, const int32_t* cur_pos, void* k_cache_bf16,
+                             int64_t cache_rows, const float* weight, const float* bias, const float* freqs,
+                             float eps, void* stream);
+
+/* The same keys quantised straight into KI pages (uint8 [n_pages, 8448]) at positions
+ * *cur_pos + t, exactly as tl_ki_cache_write would store the bf16 result (scale_mode as
+ * tl_act_quant): the producer of the page cache tl_indexer_fp8_scores_paged reads, with no
+ * bf16 round trip through memory.  Positions outside the pages are dropped. */
+int tl_layernorm_rope_rotate_ki(const void* x_bf16, int64_t seq, const int32_t* cur_pos, void* ki_pages,
+                                int64_t n_pages, const float* weight, const float* bias, const float* freqs,
+                                float eps, int scale_mode, void* stream);
 
 /* Exact per-row top-k.  logits fp32 [rows, ld]; row i considers columns
  * [0, valid_base + 1 + i) (clamped to [0, ld]) -- topk_accurate's convention with

@@ -289,3 +289,56 @@ def topk_rows(logits: torch.Tensor, valid: list[int], k: int) -> torch.Tensor:
 def _sort_desc_stable(v: torch.Tensor) -> list[int]:
     # stable sort on -v keeps ascending index among equal scores
     return torch.sort(-v, stable=True).indices.tolist()
+
+
+# ----------------------------------------------------------------- indexer key producer
+HADAMARD_SCALE_128 = torch.tensor(128 ** -0.5, dtype=torch.float32)
+
+
+def hadamard_matrix(n: int) -> torch.Tensor:
+    """Sylvester-ordered Hadamard matrix, H[i, j] = (-1)^popcount(i & j) (the ordering of
+    scipy.linalg.hadamard and of fast_hadamard_transform), fp32 +-1 entries."""
+    i = torch.arange(n)
+    bits = torch.bitwise_and(i[:, None], i[None, :])
+    parity = torch.zeros_like(bits)
+    while torch.any(bits):
+        parity ^= bits & 1
+        bits = bits >> 1
+    return (1 - 2 * parity).to(torch.float32)
+
+
+def rotate_activation(k: torch.Tensor) -> torch.Tensor:
+    """``rotate_activation`` (ops/rotate.py:17-21): fast_hadamard_transform(x, scale=d^-0.5)
+    on a bf16 [..., 128] tensor.  fast_hadamard_transform (an unpinned third-party package,
+    absent here) computes the transform in fp32 and returns the input dtype, so this is
+    bf16(fp32(H x) * fp32(128^-0.5)).  Its scipy fallback (ops/rotate.py:22-49) would run the
+    matmul in bf16 and round twice; the production path is the one restated."""
+    d = k.shape[-1]
+    h = hadamard_matrix(d)
+    y = k.float().reshape(-1, d) @ h.T
+    return (y * HADAMARD_SCALE_128).to(torch.bfloat16).reshape(k.shape)
+
+
+def rope_half(pe: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    """``apply_rotary_emb(..., interleaved=False)`` (tilert/models/utils.py:121-145) on bf16
+    [s, 64]: element i pairs with element i + 32 as the complex number (x_i, x_{i+32}),
+    which is multiplied by freqs_cis[s, i] in complex64; the result is bf16 with real parts
+    in 0..31 and imaginary parts in 32..63.  ``freqs`` is the op's fp32 [s, 64] operand
+    (view_as_real of freqs_cis: cos, sin interleaved, layernorm_rope_rotate.py:224-226)."""
+    s, d = pe.shape
+    x = pe.view(s, 2, d // 2).transpose(-1, -2).contiguous()
+    xc = torch.view_as_complex(x.float().reshape(s, d // 2, 2))
+    fc = torch.view_as_complex(freqs.float().reshape(s, d // 2, 2).contiguous())
+    y = torch.view_as_real(xc * fc).flatten(1)
+    y = torch.cat([y[..., 0::2], y[..., 1::2]], dim=-1)
+    return y.to(torch.bfloat16)
+
+
+def layernorm_rope_rotate(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                          freqs: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """``LayerNormRoPERotate.golden_forward`` (ops/layernorm_rope_rotate.py:206-220) on bf16
+    [s, 128]: k = bf16(LayerNorm(x) * weight + bias); the first 64 dims take the
+    non-interleaved RoPE; then rotate_activation (the 128-point Hadamard, scale 128^-0.5)."""
+    k = F.layer_norm(x.float(), (x.shape[-1],), weight.float(), bias.float(), eps).to(torch.bfloat16)
+    pe = rope_half(k[:, :64], freqs)
+    return rotate_activation(torch.cat([pe, k[:, 64:]], dim=-1))

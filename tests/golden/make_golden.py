@@ -65,7 +65,22 @@ def main() -> None:
     top = ref.topk_rows(logits, [510, 511], 64)
     np.savez_compressed(HERE / "indexer.npz", q_fp8=u8(q), q_s=qs.numpy(), k_fp8=u8(k), k_s=ks.numpy(),
                         w_bf16=bf(wi), cur_pos=np.array(509), logits=logits.numpy(), top64=top.numpy())
+    ki_producer()
     print("fixtures written to", HERE)
+
+
+def ki_producer() -> None:
+    """Indexer key producer (LayerNorm -> RoPE -> Hadamard): 9 keys, non-trivial norm
+    weight / bias and random RoPE angles."""
+    g = synth.gen(2025)
+    x = (torch.randn(9, 128, generator=g) * 2 + 0.3).to(torch.bfloat16)
+    w = torch.rand(128, generator=g) * 0.2 + 0.9
+    b = torch.randn(128, generator=g) * 0.1
+    theta = torch.rand(9, 32, generator=g, dtype=torch.float64) * 6.28
+    fr = torch.stack([theta.cos(), theta.sin()], dim=-1).reshape(9, 64).float()
+    k = ref.layernorm_rope_rotate(x, w, b, fr)
+    np.savez_compressed(HERE / "ki_producer.npz", x_bf16=bf(x), weight=w.numpy(), bias=b.numpy(), freqs=fr.numpy(),
+                        k_bf16=bf(k))
 
 
 if __name__ == "__main__":

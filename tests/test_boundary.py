@@ -20,7 +20,8 @@ def declared_symbols():
 def test_header_declares_the_expected_entry_points():
     names = declared_symbols()
     for n in ("tl_act_quant", "tl_fp8_gemm", "tl_fp8_gemm_packed", "tl_moe_gate_up_swiglu",
-              "tl_moe_down_combine", "tl_indexer_fp8_scores", "tl_topk_rows", "tl_last_error"):
+              "tl_moe_down_combine", "tl_indexer_fp8_scores", "tl_topk_rows", "tl_last_error",
+              "tl_layernorm_rope_rotate", "tl_layernorm_rope_rotate_ki"):
         assert n in names
 
 
@@ -53,6 +54,9 @@ def test_argument_errors_need_no_gpu():
     assert lib.tl_topk_rows(None, 4, 131072, 0, 9000, None, None, 0, None) == 3
     assert lib.tl_moe_gate_up_swiglu(None, None, None, None, 17, 8, 0, 32, 7168, 2048, None, None) == 3
     assert lib.tl_act_quant(None, None, None, 4, 100, 128, 0, None) == 1
+    assert lib.tl_layernorm_rope_rotate(None, 4, None, None, 8, None, None, None, 1e-6, None) == 1
+    assert b"null pointer" in lib.tl_last_error()
+    assert lib.tl_layernorm_rope_rotate_ki(None, 0, None, None, 1, None, None, None, 1e-6, 5, None) == 1
     assert lib.tl_fp8_gemm_workspace_bytes(32, 576, 7168) > 0  # narrow layer at M > 16: split K
     assert lib.tl_fp8_gemm_workspace_bytes(4, 576, 7168) == 0  # GEMV: never split
     assert lib.tl_fp8_gemm_workspace_bytes(4, 18432, 7168) == 0
@@ -73,6 +77,22 @@ def test_wrappers_reject_cpu_tensors():
         K.act_quant(torch.zeros(2, 100, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="topk must be"):
         topk_accurate(torch.zeros(1, 2, 8), 8, 100)
+    # layernorm_rope_rotate keeps the reference op's checks (ops/layernorm_rope_rotate.py:34-56)
+    from tilert_amd.layernorm_rope_rotate import layernorm_rope_rotate
+    x = torch.zeros(1, 2, 128, dtype=torch.bfloat16)
+    pos = torch.zeros(1, dtype=torch.int32)
+    cache = torch.zeros(1, 4, 128, dtype=torch.bfloat16)
+    w, b, f = torch.ones(128), torch.zeros(128), torch.zeros(2, 1, 64)
+    with pytest.raises(ValueError, match="input must be a bfloat16 tensor"):
+        layernorm_rope_rotate(x.float(), pos, cache, w, b, f, None, "deepseek_v3_2")
+    with pytest.raises(ValueError, match="cur_pos must be a int32 tensor"):
+        layernorm_rope_rotate(x, pos.long(), cache, w, b, f, None, "deepseek_v3_2")
+    with pytest.raises(ValueError, match="dim must be 128"):
+        layernorm_rope_rotate(torch.zeros(1, 2, 64, dtype=torch.bfloat16), pos, cache, w, b, f, None, "deepseek_v3_2")
+    with pytest.raises(ValueError, match="batch must be 1"):
+        layernorm_rope_rotate(torch.zeros(2, 2, 128, dtype=torch.bfloat16), pos, cache, w, b, f, None, "deepseek_v3_2")
+    with pytest.raises(ValueError, match="GPU"):
+        layernorm_rope_rotate(x, pos, cache, w, b, f, None, "deepseek_v3_2")
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -34,3 +34,9 @@ def test_indexer_fixture():
                             bf16(d["w_bf16"]), int(d["cur_pos"]))
     assert torch.equal(lg, f32(d["logits"]))
     assert torch.equal(ref.topk_rows(lg, [510, 511], 64), torch.from_numpy(d["top64"]))
+
+
+def test_ki_producer_fixture():
+    d = load("ki_producer")
+    k = ref.layernorm_rope_rotate(bf16(d["x_bf16"]), f32(d["weight"]), f32(d["bias"]), f32(d["freqs"]))
+    assert torch.equal(k, bf16(d["k_bf16"]))

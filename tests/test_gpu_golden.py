@@ -51,3 +51,18 @@ def test_indexer_fixture_gpu(cuda):
     idx = topk_rows(f32(d["logits"]).to(cuda), 509, 64).cpu()
     for i in range(2):  # fixture order is by score; ours is ascending column
         assert torch.equal(idx[i].sort().values, torch.from_numpy(d["top64"][i]).sort().values)
+
+
+def test_ki_producer_fixture_gpu(cuda):
+    from tilert_amd.layernorm_rope_rotate import layernorm_rope_rotate
+    d = load("ki_producer")
+    x = bf16(d["x_bf16"])
+    n = x.shape[0]
+    cache = torch.zeros(1, n, 128, dtype=torch.bfloat16, device=cuda)
+    layernorm_rope_rotate(x[None].to(cuda), torch.zeros(1, dtype=torch.int32, device=cuda), cache,
+                          f32(d["weight"]).to(cuda), f32(d["bias"]).to(cuda), f32(d["freqs"]).reshape(n, 1, 64).to(cuda),
+                          None, "deepseek_v3_2")
+    got, want = cache[0].cpu().float(), bf16(d["k_bf16"]).float()
+    e = torch.floor(torch.log2(torch.maximum(got.abs(), want.abs()).clamp_min(2.0 ** -126)))
+    assert torch.all((got - want).abs() <= torch.pow(2.0, e - 7))  # within one bf16 step
+    assert (got == want).float().mean().item() > 0.99

@@ -222,3 +222,75 @@ def test_rmsnorm_quant_is_act_quant_of_the_bf16_norm():
     y, q, s = ref.rmsnorm_quant(x, w)
     q2, s2 = ref.act_quant(y)
     assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(s, s2)
+
+
+# ------------------------------------------------- indexer key producer (LN, RoPE, Hadamard)
+def _bf16_ulp_of(t: torch.Tensor) -> torch.Tensor:
+    e = torch.floor(torch.log2(t.abs().clamp_min(2.0 ** -126)))
+    return torch.pow(2.0, e - 7)
+
+
+def test_hadamard_matrix_is_scipy_sylvester_and_orthogonal():
+    import scipy.linalg
+    h = ref.hadamard_matrix(128)
+    assert np.array_equal(h.numpy(), scipy.linalg.hadamard(128).astype(np.float32))
+    assert torch.equal(h @ h.T, 128 * torch.eye(128))
+
+
+def test_rotate_activation_vs_fp64_and_involution():
+    import scipy.linalg
+    g = synth.gen(31)
+    x = (torch.randn(64, 128, generator=g) * 3).to(torch.bfloat16)
+    y = ref.rotate_activation(x)
+    h64 = torch.tensor(scipy.linalg.hadamard(128), dtype=torch.float64)
+    want = ((x.double() @ h64.T) * 128 ** -0.5)
+    diff = (y.double() - want).abs()
+    assert torch.all(diff <= _bf16_ulp_of(want.float()).double())  # at most one bf16 rounding
+    assert (y.double() == want.to(torch.bfloat16).double()).float().mean() > 0.99
+    back = ref.rotate_activation(y)  # H / sqrt(128) is its own inverse
+    assert ((back.float() - x.float()).norm() / x.float().norm()).item() < 1e-2
+
+
+def test_rope_half_special_angles_and_fp64():
+    g = synth.gen(32)
+    pe = torch.randn(8, 64, generator=g).to(torch.bfloat16)
+    one = torch.zeros(8, 64)
+    one[:, 0::2] = 1.0
+    assert torch.equal(ref.rope_half(pe, one), pe)                     # angle 0: identity
+    quarter = torch.zeros(8, 64)
+    quarter[:, 1::2] = 1.0                                              # angle pi/2: (a, b) -> (-b, a)
+    assert torch.equal(ref.rope_half(pe, quarter), torch.cat([-pe[:, 32:], pe[:, :32]], dim=-1))
+    theta = torch.rand(8, 32, generator=g, dtype=torch.float64) * 6.28
+    fr = torch.stack([theta.cos(), theta.sin()], dim=-1).reshape(8, 64).float()
+    out = ref.rope_half(pe, fr).double()
+    a, b = pe[:, :32].double(), pe[:, 32:].double()
+    c, s = fr[:, 0::2].double(), fr[:, 1::2].double()
+    want = torch.cat([a * c - b * s, a * s + b * c], dim=-1)
+    assert torch.all((out - want).abs() <= _bf16_ulp_of(want.float()).double())
+
+
+def test_layernorm_rope_rotate_vs_fp64_brute_force():
+    import scipy.linalg
+    g = synth.gen(33)
+    s = 16
+    x = (torch.randn(s, 128, generator=g) * 2 + 0.5).to(torch.bfloat16)
+    w = torch.rand(128, generator=g) * 0.2 + 0.9
+    b = torch.randn(128, generator=g) * 0.1
+    theta = torch.rand(s, 32, generator=g, dtype=torch.float64) * 6.28
+    fr = torch.stack([theta.cos(), theta.sin()], dim=-1).reshape(s, 64).float()
+    got = ref.layernorm_rope_rotate(x, w, b, fr)
+    # fp64 restatement of golden_forward, with its two bf16 roundings (after the norm and
+    # after the RoPE) and the last one after the transform
+    xd = x.double()
+    mu = xd.mean(-1, keepdim=True)
+    var = ((xd - mu) ** 2).mean(-1, keepdim=True)
+    k = ((xd - mu) / torch.sqrt(var + 1e-6) * w.double() + b.double()).to(torch.bfloat16).double()
+    a, bb = k[:, :32], k[:, 32:64]
+    c, sn = fr[:, 0::2].double(), fr[:, 1::2].double()
+    pe = torch.cat([a * c - bb * sn, a * sn + bb * c], dim=-1).to(torch.bfloat16).double()
+    kk = torch.cat([pe, k[:, 64:]], dim=-1)
+    want = (kk @ torch.tensor(scipy.linalg.hadamard(128), dtype=torch.float64).T) * 128 ** -0.5
+    rel = ((got.double() - want).norm() / want.norm()).item()
+    assert rel < 4e-3, rel
+    # a dropped scale, a sign slip in the rotation or interleaved pairing would fail these
+    assert (got.double() - want).abs().max().item() < 0.05 * want.abs().max().item()

@@ -341,6 +341,87 @@ __global__ __launch_bounds__(256) void ki_write_kernel(const uint16_t* __restric
   }
 }
 
+
+// ------------------------------------------------------------- indexer key producer
+// LayerNormRoPERotate (ops/layernorm_rope_rotate.py:23-82, golden :206-220) for 128-wide
+// indexer keys: k = bf16(LayerNorm(x) * weight + bias) (eps as given, biased variance);
+// dims 0..63 take the non-interleaved RoPE (element i pairs with i + 32 as a complex
+// number times freqs[i] = (cos, sin), tilert/models/utils.py:121-145), rounded to bf16;
+// then the 128-point Hadamard transform with scale 128^-1/2 (rotate_activation,
+// ops/rotate.py:17-21), rounded to bf16.  One wave per token: lane l holds elements l and
+// l + 64, so the norm's sums are wave reductions, the RoPE partner of element l < 32 is
+// lane l + 32 (and back), and the transform is the within-lane butterfly (bit 6) plus six
+// cross-lane butterflies (bits 0..5).  Token t lands at row *cur_pos + t: of the bf16 key
+// cache (KI = false, the reference op's output), or quantised per token into its KI page
+// (KI = true, the format tl_ki_cache_write writes).  Rows outside the cache are dropped.
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ inline float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <bool KI>
+__global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
+    const uint16_t* __restrict__ x, int64_t seq, const int32_t* __restrict__ cur_pos, uint16_t* __restrict__ cache,
+    int64_t cache_rows, uint8_t* __restrict__ pages, const float* __restrict__ weight, const float* __restrict__ bias,
+    const float* __restrict__ freqs, float eps, int scale_mode) {
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (tok >= seq) return;  // wave-uniform
+  const uint16_t* xr = x + tok * 128;
+  const float x0 = bf16_to_f32(xr[lane]), x1 = bf16_to_f32(xr[lane + 64]);
+  const float w0 = weight[lane], w1 = weight[lane + 64], b0 = bias[lane], b1 = bias[lane + 64];
+  const int i = lane & 31;
+  const float fc = freqs[tok * 64 + 2 * i], fs = freqs[tok * 64 + 2 * i + 1];
+  const int64_t row = static_cast<int64_t>(*cur_pos) + tok;
+
+  // LayerNorm in fp32: mean, biased variance, 1 / sqrt(var + eps)
+  const float mean = wave_sum(x0 + x1) * (1.0f / 128.0f);
+  const float d0 = x0 - mean, d1 = x1 - mean;
+  const float var = wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128.0f);
+  const float rstd = 1.0f / sqrtf(var + eps);
+  float v0 = bf16_round(d0 * rstd * w0 + b0);
+  float v1 = bf16_round(d1 * rstd * w1 + b1);
+  // RoPE on elements 0..63 (v0 of every lane): (re, im) = (x_i, x_{i+32}) times (c, s)
+  const float p = __shfl_xor(v0, 32);
+  v0 = bf16_round(lane < 32 ? v0 * fc - p * fs : p * fs + v0 * fc);
+  // Hadamard: bit 6 inside the lane, bits 5..0 across lanes
+  {
+    const float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+  }
+#pragma unroll
+  for (int bit = 32; bit >= 1; bit >>= 1) {
+    const float q0 = __shfl_xor(v0, bit), q1 = __shfl_xor(v1, bit);
+    const bool hi = lane & bit;
+    v0 = hi ? q0 - v0 : v0 + q0;
+    v1 = hi ? q1 - v1 : v1 + q1;
+  }
+  constexpr float kScale = 0.08838834764831845f;  // fp32(128^-1/2)
+  const uint16_t o0 = f32_to_bf16(v0 * kScale), o1 = f32_to_bf16(v1 * kScale);
+  if (row < 0 || row >= cache_rows) return;  // wave-uniform: outside the cache
+  if constexpr (!KI) {
+    uint16_t* dst = cache + row * 128;
+    dst[lane] = o0;
+    dst[lane + 64] = o1;
+  } else {
+    // the key's act_quant over its 128 bf16 values (as ki_write_kernel)
+    const float f0 = bf16_to_f32(o0), f1 = bf16_to_f32(o1);
+    float amax = fmaxf(__builtin_fabsf(f0), __builtin_fabsf(f1));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const float sc = group_scale(amax, scale_mode);
+    uint8_t* page = pages + (row / kKiPageKeys) * kKiPageBytes;
+    const int r = static_cast<int>(row % kKiPageKeys);
+    page[r * 128 + lane] = static_cast<uint8_t>(f32_to_e4m3(fminf(fmaxf(f0 / sc, -kE4m3Max), kE4m3Max)));
+    page[r * 128 + lane + 64] = static_cast<uint8_t>(f32_to_e4m3(fminf(fmaxf(f1 / sc, -kE4m3Max), kE4m3Max)));
+    if (lane == 0) *reinterpret_cast<float*>(page + kKiPageKeys * 128 + r * 4) = sc;
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
@@ -378,4 +459,38 @@ extern "C" int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_page
   hipLaunchKernelGGL(ki_write_kernel, dim3(cdiv(rows * 16, 256)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)k_bf16, (uint8_t*)ki_pages, rows, pos, scale_mode);
   return check_launch("ki_cache_write");
+}
+
+static int ln_rope_rotate_check(const char* who, const void* x, int64_t seq, const int32_t* cur_pos, const void* out,
+                                const float* weight, const float* bias, const float* freqs) {
+  if (seq < 0 || seq > (1ll << 24)) { set_error("%s: seq=%lld out of range", who, (long long)seq); return kErrArg; }
+  if (!x || !cur_pos || !out || !weight || !bias || !freqs) { set_error("%s: null pointer", who); return kErrArg; }
+  return kOk;
+}
+
+extern "C" int tl_layernorm_rope_rotate(const void* x_bf16, int64_t seq, const int32_t* cur_pos, void* k_cache_bf16,
+                                        int64_t cache_rows, const float* weight, const float* bias, const float* freqs,
+                                        float eps, void* stream) {
+  if (int rc = ln_rope_rotate_check("layernorm_rope_rotate", x_bf16, seq, cur_pos, k_cache_bf16, weight, bias, freqs))
+    return rc;
+  if (cache_rows < 0) { set_error("layernorm_rope_rotate: cache_rows=%lld", (long long)cache_rows); return kErrArg; }
+  if (seq == 0) return kOk;
+  hipLaunchKernelGGL(ln_rope_rotate_kernel<false>, dim3(static_cast<unsigned>(cdiv(seq, 4))), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, seq, cur_pos, (uint16_t*)k_cache_bf16, cache_rows,
+                     nullptr, weight, bias, freqs, eps, 0);
+  return check_launch("layernorm_rope_rotate");
+}
+
+extern "C" int tl_layernorm_rope_rotate_ki(const void* x_bf16, int64_t seq, const int32_t* cur_pos, void* ki_pages,
+                                           int64_t n_pages, const float* weight, const float* bias, const float* freqs,
+                                           float eps, int scale_mode, void* stream) {
+  if (int rc = ln_rope_rotate_check("layernorm_rope_rotate_ki", x_bf16, seq, cur_pos, ki_pages, weight, bias, freqs))
+    return rc;
+  if (n_pages < 0) { set_error("layernorm_rope_rotate_ki: n_pages=%lld", (long long)n_pages); return kErrArg; }
+  if (scale_mode < 0 || scale_mode > 2) { set_error("layernorm_rope_rotate_ki: bad scale_mode %d", scale_mode); return kErrArg; }
+  if (seq == 0) return kOk;
+  hipLaunchKernelGGL(ln_rope_rotate_kernel<true>, dim3(static_cast<unsigned>(cdiv(seq, 4))), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x_bf16, seq, cur_pos, nullptr, n_pages * kKiPageKeys,
+                     (uint8_t*)ki_pages, weight, bias, freqs, eps, scale_mode);
+  return check_launch("layernorm_rope_rotate_ki");
 }
