@@ -13,7 +13,7 @@ repeat reads.
 
 ``--extras`` adds (outside the JSON contract's required keys, under "extras") the MLA
 projections (config 1), the MoE layer (config 2), the M sweep (config 3) and the
-indexer + top-k at 128K (config 4), and the indexer key producer.
+indexer + top-k at 128K (config 4), the indexer key producer and sparse MLA attention.
 """
 from __future__ import annotations
 
@@ -292,6 +292,29 @@ def extras(torch, steps, dev):
         si.ki_cache_write(kcache[0, L - 4:], kpages, L - 4)
     us_2 = _graph_time_us(torch, two_step, st, 5)
     out["ki_producer_M4"] = {"fused_us": round(us_f, 2), "bf16_cache_then_page_write_us": round(us_2, 2)}
+    del kpages, kcache
+
+    # sparse MLA decode attention over the top-2048 of a 128K latent cache: 4 tokens x 16
+    # heads (TP=8 share), independent selections per token, 3 rotating caches (> MALL)
+    from tilert_amd.flash_sparse_mla import flash_sparse_mla
+    T, Hm, km = L, 16, 2048
+    gm = torch.Generator(device=dev).manual_seed(5)
+    kvs = [(torch.randn(1, T, 512, device=dev, generator=gm).to(torch.bfloat16),
+            torch.randn(1, T, 64, device=dev, generator=gm).to(torch.bfloat16)) for _ in range(3)]
+    qm = (torch.randn(1, M, Hm, 512, device=dev, generator=gm) * 0.5).to(torch.bfloat16)
+    qpm = (torch.randn(1, M, Hm, 64, device=dev, generator=gm) * 0.5).to(torch.bfloat16)
+    im = torch.stack([torch.randperm(T - 4, device=dev, generator=gm)[:km] for _ in range(M)]).to(torch.int32)[None]
+    om = torch.empty(1, M, Hm, 512, dtype=torch.bfloat16, device=dev)
+    pm = torch.tensor([T - 4], dtype=torch.int32, device=dev)
+    us_m = _graph_time_us(torch, lambda i: flash_sparse_mla(qm, qpm, kvs[i % 3][0], kvs[i % 3][1], im, pm, om, None,
+                                                            model_arch="deepseek_v3_2"), st, 5)
+    gathered = M * km * (512 + 64) * 2
+    acc = 2 * M * Hm * 32 * 512 * 4  # output_acc written by the split kernel, read by the combine
+    out["sparse_mla_128k_M4"] = {"us": round(us_m, 2), "gathered_bytes": gathered,
+                                 "gathered_GBs": round(gathered / us_m / 1e3, 1),
+                                 "all_bytes_GBs": round((gathered + acc + qm.numel() * 2 * 2) / us_m / 1e3, 1),
+                                 "hbm_frac_gathered": round(gathered / us_m / 1e3 / HBM_PEAK_GBS, 3)}
+    del kvs
     return out
 
 

@@ -31,6 +31,8 @@
  *                                (golden :206-220)
  *   tl_layernorm_rope_rotate_ki  the same, its keys quantised into KI pages (the producer of
  *                                the format tl_indexer_fp8_scores_paged reads)
+ *   tl_flash_sparse_mla    flash_sparse_mla_op            .../ops/flash_sparse_mla.py:18-93
+ *                          (golden FlashSparseMLACombine.golden_forward :152-196)
  *   tl_topk_rows           topk_accurate_op               .../ops/topk.py:62-109
  *   (sparse_index_topk_dsv32_op, .../ops/sparse_index.py:72-128, = scores + top-k)
  */
@@ -221,6 +223,25 @@ int tl_layernorm_rope_rotate(const void* x_bf16, int64_t seq, const int32_t* cur
 int tl_layernorm_rope_rotate_ki(const void* x_bf16, int64_t seq, const int32_t* cur_pos, void* ki_pages,
                                 int64_t n_pages, const float* weight, const float* bias, const float* freqs,
                                 float eps, int scale_mode, void* stream);
+
+/* Sparse MLA decode attention over the indexer's selection, flash_sparse_mla_op
+ * (ops/flash_sparse_mla.py:18-93; golden :152-196).  q_nope bf16 [seqlen, heads, 512],
+ * q_pe bf16 [seqlen, heads, 64], kv bf16 [kv_rows, 512], pe bf16 [kv_rows, 64], indices int32
+ * [seqlen, topk] (distinct positions; entries outside [0, kv_rows) are ignored), cur_pos
+ * device int32.  For token s and head h: softmax over the selected positions t of
+ * (q_nope . kv[t] + q_pe . pe[t]) * softmax_scale (fp32; for seqlen > 1 positions after
+ * *cur_pos + s are masked too), probabilities as bf16, times kv[t], fp32 accumulation ->
+ * out bf16 [seqlen, heads, 512].  Split-K over ceil(topk / 64) <= 32 splits of 64 positions:
+ * out_acc fp32 [seqlen, heads, 32, 512] receives each split's normalised output, lse_acc
+ * fp32 [seqlen, heads, 32] its ln-sum-exp (-inf for a split with nothing visible), lse fp32
+ * [seqlen, heads] the total (the reference op's output_acc / lse_acc / lse; a token with no
+ * visible position gets zeros and -inf).  1 <= seqlen <= 16, 1 <= heads <= 32,
+ * 1 <= topk <= 2048. */
+int tl_flash_sparse_mla(const void* q_nope_bf16, const void* q_pe_bf16, const void* kv_bf16,
+                        const void* pe_bf16, const int32_t* indices, const int32_t* cur_pos,
+                        int64_t seqlen, int64_t heads, int64_t topk, int64_t kv_rows,
+                        float softmax_scale, void* out_bf16, float* out_acc, float* lse,
+                        float* lse_acc, void* stream);
 
 /* Exact per-row top-k.  logits fp32 [rows, ld]; row i considers columns
  * [0, valid_base + 1 + i) (clamped to [0, ld]) -- topk_accurate's convention with

@@ -342,3 +342,34 @@ def layernorm_rope_rotate(x: torch.Tensor, weight: torch.Tensor, bias: torch.Ten
     k = F.layer_norm(x.float(), (x.shape[-1],), weight.float(), bias.float(), eps).to(torch.bfloat16)
     pe = rope_half(k[:, :64], freqs)
     return rotate_activation(torch.cat([pe, k[:, 64:]], dim=-1))
+
+
+# ------------------------------------------------------------------ sparse MLA attention
+def mla_softmax_scale(model_arch: str) -> float:
+    """FlashSparseMLACombine.softmax_scale (ops/flash_sparse_mla.py:125-130):
+    (qk_nope_head_dim + qk_rope_head_dim)^-1/2 * mscale^2, mscale = 0.1 ln(rope_factor) + 1
+    (1 without a rope factor).  deepseek_v3_2: 128 + 64, rope_factor 40
+    (deepseek_v3_2/model_args.py:76-82); glm_5: 192 + 64, no rope factor
+    (glm_5/model_args.py:42-48)."""
+    nope, rope, factor = {"deepseek_v3_2": (128, 64, 40.0), "glm_5": (192, 64, None)}[model_arch]
+    mscale = 1.0 if factor is None else 0.1 * math.log(factor) + 1.0
+    return (nope + rope) ** -0.5 * mscale * mscale
+
+
+def flash_sparse_mla(q_nope: torch.Tensor, q_pe: torch.Tensor, kv: torch.Tensor, pe: torch.Tensor,
+                     indices: torch.Tensor, cur_pos: int, softmax_scale: float) -> torch.Tensor:
+    """``FlashSparseMLACombine.golden_forward`` (ops/flash_sparse_mla.py:152-196) for batch 1:
+    q_nope bf16 [s, h, 512], q_pe bf16 [s, h, 64], kv bf16 [T, 512], pe bf16 [T, 64], indices
+    int [s, topk] (distinct positions).  scores = (q_nope . kv + q_pe . pe) * scale in fp32;
+    every position not in the token's indices is -inf, and for s > 1 also every position
+    after cur_pos + token (the triu mask); softmax in fp32, probabilities rounded to bf16,
+    times kv -> bf16 [s, h, 512]."""
+    s, h, _ = q_nope.shape
+    T = kv.shape[0]
+    scores = (torch.einsum("shc,tc->sht", q_nope.float(), kv.float())
+              + torch.einsum("shr,tr->sht", q_pe.float(), pe.float())) * softmax_scale
+    index_mask = torch.full((s, T), float("-inf")).scatter_(-1, indices.long(), 0)
+    if s > 1:
+        index_mask += torch.full((s, T), float("-inf")).triu_(cur_pos + 1)
+    scores = (scores + index_mask[:, None, :]).softmax(dim=-1, dtype=torch.float32)
+    return torch.einsum("sht,tc->shc", scores.to(torch.bfloat16), kv)

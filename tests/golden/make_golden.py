@@ -66,6 +66,7 @@ def main() -> None:
     np.savez_compressed(HERE / "indexer.npz", q_fp8=u8(q), q_s=qs.numpy(), k_fp8=u8(k), k_s=ks.numpy(),
                         w_bf16=bf(wi), cur_pos=np.array(509), logits=logits.numpy(), top64=top.numpy())
     ki_producer()
+    sparse_mla()
     print("fixtures written to", HERE)
 
 
@@ -81,6 +82,20 @@ def ki_producer() -> None:
     k = ref.layernorm_rope_rotate(x, w, b, fr)
     np.savez_compressed(HERE / "ki_producer.npz", x_bf16=bf(x), weight=w.numpy(), bias=b.numpy(), freqs=fr.numpy(),
                         k_bf16=bf(k))
+
+
+def sparse_mla() -> None:
+    """Sparse MLA attention: 2 tokens, 8 heads, 100 of 160 positions selected per token
+    (two splits, the second partial), glm_5's softmax scale."""
+    g = synth.gen(2026)
+    q = (torch.randn(2, 8, 512, generator=g) * 0.5).to(torch.bfloat16)
+    qp = (torch.randn(2, 8, 64, generator=g) * 0.5).to(torch.bfloat16)
+    kv = torch.randn(160, 512, generator=g).to(torch.bfloat16)
+    pe = torch.randn(160, 64, generator=g).to(torch.bfloat16)
+    idx = torch.stack([torch.randperm(159, generator=g)[:100] for _ in range(2)]).to(torch.int32)
+    out = ref.flash_sparse_mla(q, qp, kv, pe, idx, 158, ref.mla_softmax_scale("glm_5"))
+    np.savez_compressed(HERE / "sparse_mla.npz", q_bf16=bf(q), qpe_bf16=bf(qp), kv_bf16=bf(kv), pe_bf16=bf(pe),
+                        indices=idx.numpy(), cur_pos=np.array(158), out_bf16=bf(out))
 
 
 if __name__ == "__main__":

@@ -40,3 +40,10 @@ def test_ki_producer_fixture():
     d = load("ki_producer")
     k = ref.layernorm_rope_rotate(bf16(d["x_bf16"]), f32(d["weight"]), f32(d["bias"]), f32(d["freqs"]))
     assert torch.equal(k, bf16(d["k_bf16"]))
+
+
+def test_sparse_mla_fixture():
+    d = load("sparse_mla")
+    out = ref.flash_sparse_mla(bf16(d["q_bf16"]), bf16(d["qpe_bf16"]), bf16(d["kv_bf16"]), bf16(d["pe_bf16"]),
+                               torch.from_numpy(d["indices"]), int(d["cur_pos"]), ref.mla_softmax_scale("glm_5"))
+    assert torch.equal(out, bf16(d["out_bf16"]))

@@ -66,3 +66,14 @@ def test_ki_producer_fixture_gpu(cuda):
     e = torch.floor(torch.log2(torch.maximum(got.abs(), want.abs()).clamp_min(2.0 ** -126)))
     assert torch.all((got - want).abs() <= torch.pow(2.0, e - 7))  # within one bf16 step
     assert (got == want).float().mean().item() > 0.99
+
+
+def test_sparse_mla_fixture_gpu(cuda):
+    from tilert_amd.flash_sparse_mla import flash_sparse_mla
+    d = load("sparse_mla")
+    q = bf16(d["q_bf16"])
+    out = torch.zeros(1, *q.shape, dtype=torch.bfloat16, device=cuda)
+    flash_sparse_mla(q[None].to(cuda), bf16(d["qpe_bf16"])[None].to(cuda), bf16(d["kv_bf16"])[None].to(cuda),
+                     bf16(d["pe_bf16"])[None].to(cuda), torch.from_numpy(d["indices"])[None].to(cuda),
+                     torch.tensor([int(d["cur_pos"])], dtype=torch.int32, device=cuda), out, None, model_arch="glm_5")
+    assert_gemm_close(out[0], bf16(d["out_bf16"]), "sparse_mla fixture")

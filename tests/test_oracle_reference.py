@@ -294,3 +294,62 @@ def test_layernorm_rope_rotate_vs_fp64_brute_force():
     assert rel < 4e-3, rel
     # a dropped scale, a sign slip in the rotation or interleaved pairing would fail these
     assert (got.double() - want).abs().max().item() < 0.05 * want.abs().max().item()
+
+
+# --------------------------------------------------------------- sparse MLA attention
+def _mla_inputs(s, h, T, g):
+    q = (torch.randn(s, h, 512, generator=g) * 0.5).to(torch.bfloat16)
+    qp = (torch.randn(s, h, 64, generator=g) * 0.5).to(torch.bfloat16)
+    kv = torch.randn(T, 512, generator=g).to(torch.bfloat16)
+    pe = torch.randn(T, 64, generator=g).to(torch.bfloat16)
+    return q, qp, kv, pe
+
+
+def test_mla_softmax_scale_closed_form():
+    assert ref.mla_softmax_scale("glm_5") == 1 / 16
+    ms = 0.1 * math.log(40) + 1
+    assert abs(ref.mla_softmax_scale("deepseek_v3_2") - ms * ms / math.sqrt(192)) < 1e-15
+
+
+def test_flash_sparse_mla_vs_fp64_brute_force():
+    g = synth.gen(41)
+    s, h, T, k = 3, 16, 200, 48
+    q, qp, kv, pe = _mla_inputs(s, h, T, g)
+    idx = torch.stack([torch.randperm(T, generator=g)[:k] for _ in range(s)])
+    cur = T - s
+    sc = 0.1352
+    got = ref.flash_sparse_mla(q, qp, kv, pe, idx, cur, sc).double()
+    want = torch.zeros(s, h, 512, dtype=torch.float64)
+    for t in range(s):
+        sel = [int(i) for i in idx[t] if int(i) <= cur + t]  # s > 1: the triu mask
+        kd, pd = kv[sel].double(), pe[sel].double()
+        for hh in range(h):
+            z = (kd @ q[t, hh].double() + pd @ qp[t, hh].double()) * sc
+            p = torch.softmax(z, 0).to(torch.bfloat16).double()
+            want[t, hh] = p @ kd
+    assert ((got - want).norm() / want.norm()).item() < 2e-3
+    assert (got - want).abs().max().item() < 2 * 2.0 ** -7 * want.abs().max().item()
+
+
+def test_flash_sparse_mla_special_cases():
+    g = synth.gen(42)
+    q, qp, kv, pe = _mla_inputs(1, 8, 64, g)
+    # one selected position: its probability is exactly 1, the output is that kv row
+    out = ref.flash_sparse_mla(q, qp, kv, pe, torch.tensor([[17]]), 63, 0.1)
+    assert torch.equal(out[0], kv[17].expand(8, 512))
+    # zero queries: uniform weights 1/4 (exact in bf16) over 4 positions -> their mean
+    z = torch.zeros_like(q), torch.zeros_like(qp)
+    sel = [3, 9, 40, 41]
+    out = ref.flash_sparse_mla(*z, kv, pe, torch.tensor([sel]), 63, 0.1)
+    assert torch.equal(out[0, 0], (kv[sel].double().sum(0) / 4).to(torch.bfloat16))
+    # the order of the indices does not matter
+    idx = torch.randperm(64, generator=g)[:20][None]
+    a = ref.flash_sparse_mla(q, qp, kv, pe, idx, 63, 0.1)
+    b = ref.flash_sparse_mla(q, qp, kv, pe, idx.flip(-1), 63, 0.1)
+    assert torch.equal(a, b)
+    # two tokens: position cur_pos + 1 is visible to token 1 only
+    q2, qp2, _, _ = _mla_inputs(2, 8, 64, g)
+    two = ref.flash_sparse_mla(q2, qp2, kv, pe, torch.tensor([[5, 31], [5, 31]]), 30, 0.1)
+    only5 = ref.flash_sparse_mla(q2[:1], qp2[:1], kv, pe, torch.tensor([[5]]), 30, 0.1)
+    assert torch.equal(two[0], only5[0])
+    assert not torch.equal(two[1], ref.flash_sparse_mla(q2[1:], qp2[1:], kv, pe, torch.tensor([[5]]), 30, 0.1)[0])
