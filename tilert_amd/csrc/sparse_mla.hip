@@ -17,7 +17,7 @@
 //                  them with the split's kv rows (each wave 8 of the 32 16-wide value
 //                  tiles).  Stores output_acc[s,h,j] = O_j / l_j and lse_acc[s,h,j] =
 //                  max_j + ln l_j (-inf for a split with no visible position).
-//   combine kernel one workgroup per (head, token): lse = ln sum_j e^lse_j, out = sum_j
+//   combine kernel one workgroup per (head, token, 128 dims): lse = ln sum_j e^lse_j, out = sum_j
 //                  e^(lse_j - lse) output_acc_j, rounded to bf16.
 // Reading the gathered rows once from LDS serves both products, so every selected row is
 // read from memory once.
@@ -52,6 +52,22 @@ struct MlaLds {
 
 __device__ inline v8bf_t lds_v8bf(const uint8_t* p) { return *reinterpret_cast<const v8bf_t*>(p); }
 
+// Max / sum over each 16-lane row with DPP (no LDS round trip): swaps within quads, then
+// the half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i) pair every lane
+// with one in the other half; after each step all lanes of the group hold its result.
+template <int CTRL, bool MAX>
+__device__ inline float dpp_combine(float x) {
+  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+  return MAX ? fmaxf(x, y) : x + y;
+}
+template <bool MAX>
+__device__ inline float row16_reduce(float v) {
+  v = dpp_combine<0xb1, MAX>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_combine<0x4e, MAX>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_combine<0x141, MAX>(v);  // row_half_mirror
+  return dpp_combine<0x140, MAX>(v);  // row_mirror
+}
+
 template <int HT>
 __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     const uint16_t* __restrict__ q_nope, const uint16_t* __restrict__ q_pe, const uint16_t* __restrict__ kv,
@@ -66,25 +82,33 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
   const int r = lane & 15, g = lane >> 4;
   int32_t* idx_l = reinterpret_cast<int32_t*>(smem + S::IDX_OFF);
 
-  // the split's positions; a masked one (past topk, outside [0, T), or after the token's
-  // position when seqlen > 1) is stored as -1
-  if (tid < kMlaSplit) {
-    const int j = split * kMlaSplit + tid;
-    int t = j < topk ? indices[static_cast<int64_t>(s) * topk + j] : -1;
-    if (t < 0 || t >= T) t = -1;
-    if (seqlen > 1 && t > *cur_pos + s) t = -1;
-    idx_l[tid] = t;
-  }
-  // queries of token s: rows h < heads (rows past them are zero), 576 bf16 each
+  // the split's positions and the token's queries, loaded together: a masked position
+  // (past topk, outside [0, T), or after the token's position when seqlen > 1) is stored
+  // as -1; query rows h < heads, 576 bf16 each (rows past them zero), as 16-byte chunks
+  constexpr int QCH = HT * 16 * 72;  // 64 chunks of q_nope + 8 of q_pe per head
+  constexpr int QPT = (QCH + kMlaThreads - 1) / kMlaThreads;
+  int t_idx = -1;
   {
-    constexpr int QCH = HT * 16 * 72;  // 16-byte chunks: 64 of q_nope + 8 of q_pe per head
-    for (int c = tid; c < QCH; c += kMlaThreads) {
-      const int h = c / 72, k = c % 72;
-      u32x4s v = {0u, 0u, 0u, 0u};
-      if (h < heads)
-        v = k < 64 ? reinterpret_cast<const u32x4s*>(q_nope + (static_cast<int64_t>(s) * heads + h) * kMlaDim)[k]
+    const int j = split * kMlaSplit + min(tid, kMlaSplit - 1);
+    t_idx = indices[static_cast<int64_t>(s) * topk + min(j, topk - 1)];
+    if (j >= topk || t_idx < 0 || t_idx >= T || (seqlen > 1 && t_idx > *cur_pos + s)) t_idx = -1;
+  }
+  u32x4s qv[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int c = min(tid + u * kMlaThreads, QCH - 1);
+    const int h = min(c / 72, heads - 1), k = c % 72;
+    qv[u] = k < 64 ? reinterpret_cast<const u32x4s*>(q_nope + (static_cast<int64_t>(s) * heads + h) * kMlaDim)[k]
                    : reinterpret_cast<const u32x4s*>(q_pe + (static_cast<int64_t>(s) * heads + h) * kMlaPe)[k - 64];
-      *reinterpret_cast<u32x4s*>(smem + S::Q_OFF + h * (kMlaDim + kMlaPe) * 2 + k * 16) = v;
+  }
+  if (tid < kMlaSplit) idx_l[tid] = t_idx;
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int c = tid + u * kMlaThreads;
+    if (c < QCH) {
+      const int h = c / 72, k = c % 72;
+      const u32x4s z = {0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4s*>(smem + S::Q_OFF + h * (kMlaDim + kMlaPe) * 2 + k * 16) = h < heads ? qv[u] : z;
     }
   }
   __syncthreads();
@@ -142,11 +166,9 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
   for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = live ? sc[ht][i] * scale : -INFINITY;
+      const float v = live ? sc[ht][i] * scale : -INFINITY;
       sc[ht][i] = v;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
-      mx[ht][i] = v;
+      mx[ht][i] = row16_reduce<true>(v);
     }
   if (r == 0) {
 #pragma unroll
@@ -174,10 +196,7 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     for (int i = 0; i < 4; ++i) {
       const float p = (m[ht][i] == -INFINITY || sc[ht][i] == -INFINITY) ? 0.f : expf(sc[ht][i] - m[ht][i]);
       P[(ht * 16 + 4 * g + i) * kMlaSplit + wave * 16 + r] = f32_to_bf16(p);
-      float v = p;
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o);
-      sm[ht][i] = v;
+      sm[ht][i] = row16_reduce<false>(p);
     }
   if (r == 0) {
 #pragma unroll
@@ -236,30 +255,41 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
   (void)n_splits;
 }
 
-// One 128-thread workgroup per (head, token): 4 dims per thread.
-__global__ __launch_bounds__(128) void sparse_mla_combine_kernel(const float* __restrict__ out_acc,
-                                                                 const float* __restrict__ lse_acc, int heads,
-                                                                 int n_splits, uint16_t* __restrict__ out,
-                                                                 float* __restrict__ lse) {
-  const int h = blockIdx.x, s = blockIdx.y, tid = threadIdx.x;
+// One 64-thread workgroup per (head, token, quarter of the 512 dims): 2 dims per thread;
+// the 32 split rows are loaded together (unconditional, clamped; splits past n_splits
+// weigh 0).
+__global__ __launch_bounds__(64) void sparse_mla_combine_kernel(const float* __restrict__ out_acc,
+                                                                const float* __restrict__ lse_acc, int heads,
+                                                                int n_splits, uint16_t* __restrict__ out,
+                                                                float* __restrict__ lse) {
+  const int h = blockIdx.x, s = blockIdx.y, quarter = blockIdx.z, tid = threadIdx.x;
   const int64_t row = static_cast<int64_t>(s) * heads + h;
+  const int d0 = quarter * 128 + 2 * tid;
   const float* la = lse_acc + row * kMlaMaxSplits;
+  float2 v[kMlaMaxSplits];
+#pragma unroll
+  for (int j = 0; j < kMlaMaxSplits; ++j)
+    v[j] = *reinterpret_cast<const float2*>(out_acc + (row * kMlaMaxSplits + min(j, n_splits - 1)) * kMlaDim + d0);
+  float lj[kMlaMaxSplits];
+#pragma unroll
+  for (int j = 0; j < kMlaMaxSplits; ++j) lj[j] = j < n_splits ? la[min(j, n_splits - 1)] : -INFINITY;
   float mx = -INFINITY;
-  for (int j = 0; j < n_splits; ++j) mx = fmaxf(mx, la[j]);
+#pragma unroll
+  for (int j = 0; j < kMlaMaxSplits; ++j) mx = fmaxf(mx, lj[j]);
   float sum = 0.f;
-  for (int j = 0; j < n_splits; ++j) sum += la[j] == -INFINITY ? 0.f : expf(la[j] - mx);
+#pragma unroll
+  for (int j = 0; j < kMlaMaxSplits; ++j) sum += lj[j] == -INFINITY ? 0.f : expf(lj[j] - mx);
   const float L = mx == -INFINITY ? -INFINITY : mx + logf(sum);
-  v4f acc = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < n_splits; ++j) {
-    const float wj = (la[j] == -INFINITY) ? 0.f : expf(la[j] - L);
-    const v4f v = reinterpret_cast<const v4f*>(out_acc + (row * kMlaMaxSplits + j) * kMlaDim)[tid];
-    acc += v * wj;
+  float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMlaMaxSplits; ++j) {
+    const float wj = lj[j] == -INFINITY ? 0.f : expf(lj[j] - L);
+    a0 += v[j].x * wj;
+    a1 += v[j].y * wj;
   }
-  uint2 packed;
-  packed.x = f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16);
-  packed.y = f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16);
-  reinterpret_cast<uint2*>(out + row * kMlaDim)[tid] = packed;
-  if (tid == 0) lse[row] = L;
+  reinterpret_cast<uint32_t*>(out + row * kMlaDim + d0)[0] =
+      f32_to_bf16(a0) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
+  if (quarter == 0 && tid == 0) lse[row] = L;
 }
 
 }  // namespace tl
@@ -298,7 +328,7 @@ extern "C" int tl_flash_sparse_mla(const void* q_nope_bf16, const void* q_pe_bf1
     return check_launch("flash_sparse_mla");
   };
   if (int rc = heads <= 16 ? launch(std::integral_constant<int, 1>{}) : launch(std::integral_constant<int, 2>{})) return rc;
-  hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(seqlen)), dim3(128),
+  hipLaunchKernelGGL(sparse_mla_combine_kernel, dim3(static_cast<unsigned>(heads), static_cast<unsigned>(seqlen), 4), dim3(64),
                      0, st, out_acc, lse_acc, (int)heads, n_splits, (uint16_t*)out_bf16, lse);
   return check_launch("flash_sparse_mla");
 }
