@@ -184,10 +184,36 @@ def extras(torch, steps, dev):
                                                      model_arch="deepseek_v3_2"), st, 5)
     b = gemm_bytes(4, 2112, 7168)
     fused_us = tot_us - per["wq_a"]["us"] - per["wkv_a"]["us"] + us
+    # q RMSNorm + wq_b in one launch (RmsnormProjqWqb, BF16MMA) against RMSNorm + act_quant
+    # followed by the FP8 GEMV
+    from tilert_amd.rmsnorm_projq_wqb import rmsnorm_projq_wqb_op
+    qb_w = []
+    for c in range(8):
+        g = torch.Generator(device=dev).manual_seed(200 + c)
+        qb_w.append(K_.pack_weight(*K_.weight_quant(torch.randn(3072, 1536, device=dev, generator=g) * 0.02)))
+    qa = torch.randn(1, 4, 1536, device=dev).to(torch.bfloat16)
+    qn_w = torch.rand(1536, device=dev) + 0.5
+    q_nope = torch.empty(1, 4, 16, 128, dtype=torch.bfloat16, device=dev)
+    q_pe = torch.empty(1, 4, 16, 64, dtype=torch.bfloat16, device=dev)
+    us_pq = _graph_time_us(torch, lambda i: rmsnorm_projq_wqb_op(qa, qb_w[i % 8], None, qn_w, q_nope, q_pe, None,
+                                                                 "bf16mma", "deepseek_v3_2"), st, 5)
+    qn_b = torch.empty(1, 4, 1536, dtype=torch.bfloat16, device=dev)
+    qn_q = torch.empty(1, 4, 1536, dtype=torch.float8_e4m3fn, device=dev)
+    qn_s = torch.empty(1, 4, 12, dtype=torch.float32, device=dev)
+    qb_out = torch.empty(4, 3072, dtype=torch.bfloat16, device=dev)
+
+    def two_launch(i):
+        rmsnorm_quant(qa, qn_w, qn_b, qn_q, qn_s, logs, model_arch="deepseek_v3_2")
+        K_.fp8_gemm(qn_q.view(4, 1536), qn_s.view(4, 12), qb_w[i % 8], out=qb_out)
+    us_pq2 = _graph_time_us(torch, two_launch, st, 5)
+    b_pq = 3072 * 1536 + 24 * 12 * 4 + 4 * 1536 * 2 + 1536 * 4 + 4 * 3072 * 2
+    pq = {"us": round(us_pq, 2), "GBs": round(b_pq / us_pq / 1e3, 1),
+          "rmsnorm_quant_then_fp8_gemv_us": round(us_pq2, 2)}
     out["mla_projections_M4"] = {"layers": per, "us_total": round(tot_us, 2),
                                  "GBs": round(tot_b / tot_us / 1e3, 1),
                                  "hbm_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 3),
                                  "projx_wqkva": {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)},
+                                 "rmsnorm_projq_wqb": pq,
                                  "us_total_with_projx": round(fused_us, 2),
                                  "hbm_frac_with_projx": round(tot_b / fused_us / 1e3 / HBM_PEAK_GBS, 3)}
 

@@ -21,6 +21,7 @@
  *                       unproj_o_allreduce_op, rmsnorm_up_gate_silu_op, down_allreduce_op
  *   tl_fp8_pack_weight  the per-op weight converters (load-time layout change)
  *   tl_projx_wqkva      projx_wqkva_op       .../ops/projx_wqkva.py:22-48 (golden :268-294)
+ *   tl_rmsnorm_projq_wqb  rmsnorm_proj_qb_op  .../ops/rmsnorm_projq_wqb.py:20-44 (golden :496-512)
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
  *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
@@ -202,6 +203,18 @@ int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per
  * (ops/layernorm_rope_rotate.py:206-220) happens upstream.  pos + rows <= 64 * n_pages. */
 int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t n_pages, int64_t pos,
                       int scale_mode, void* stream);
+
+/* RMSNorm of the q latent + wq_b, RmsnormProjqWqb (ops/rmsnorm_projq_wqb.py:20-44, golden
+ * :496-512, BF16MMA): qr = bf16(q * rsqrt(mean(q^2) + eps) * q_norm_weight) in fp32 for the M
+ * rows of q bf16 [M, q_rank]; out = qr . W^T with W = bf16(fp32(wq_b) * block scale) (the
+ * golden's bf16 dequantised weight), fp32 accumulation, bf16 result, written per head as
+ * q_nope [M, heads, nope_dim] and q_pe [M, heads, rope_dim] (feature h * (nope + rope) + d
+ * of the weight is head h, dim d).  wq_b_packed: the [heads * (nope + rope), q_rank] e4m3fn
+ * weight in tl_fp8_pack_weight's layout; wq_b_s its fp32 [N/128, q_rank/128] scales.
+ * 1 <= M <= 16, q_rank % 512 == 0 and <= 2048, nope/rope multiples of 16. */
+int tl_rmsnorm_projq_wqb(const void* q_bf16, const float* q_norm_weight, float eps, const void* wq_b_packed,
+                         const float* wq_b_s, void* q_nope_bf16, void* q_pe_bf16, int64_t M, int64_t heads,
+                         int64_t q_rank, int64_t nope_dim, int64_t rope_dim, void* stream);
 
 /* Indexer key producer, LayerNormRoPERotate (ops/layernorm_rope_rotate.py:23-82, golden
  * :206-220): for each of `seq` bf16 keys x [seq, 128], k = bf16(LayerNorm(x) * weight +

@@ -373,3 +373,17 @@ def flash_sparse_mla(q_nope: torch.Tensor, q_pe: torch.Tensor, kv: torch.Tensor,
         index_mask += torch.full((s, T), float("-inf")).triu_(cur_pos + 1)
     scores = (scores + index_mask[:, None, :]).softmax(dim=-1, dtype=torch.float32)
     return torch.einsum("sht,tc->shc", scores.to(torch.bfloat16), kv)
+
+
+# ------------------------------------------------------- q RMSNorm + wq_b (BF16MMA)
+def rmsnorm_projq_wqb(q: torch.Tensor, q_norm_weight: torch.Tensor, wq_b: torch.Tensor, wq_b_s: torch.Tensor,
+                      n_heads: int, nope_dim: int = 128, rope_dim: int = 64, eps: float = 1e-6):
+    """``RmsnormProjqWqb.golden_forward`` (ops/rmsnorm_projq_wqb.py:496-512): qr =
+    bf16(rms_norm(q fp32, weight, eps)); out = qr @ weight_dequant(wq_b)^T with the weight
+    dequantised to bf16 (``init_random_weights`` :463-474 builds ``ref_wq_b`` that way) and
+    the product in bf16 (fp32 accumulation, bf16 result); split per head into q_nope
+    [..., n_heads, nope_dim] and q_pe [..., n_heads, rope_dim].  q bf16 [s, q_lora_rank]."""
+    qr = F.rms_norm(q.float(), [q.shape[-1]], q_norm_weight.float(), eps).to(torch.bfloat16)
+    w = weight_dequant(wq_b, wq_b_s).to(torch.bfloat16)
+    out = torch.matmul(qr, w.T).view(*q.shape[:-1], n_heads, nope_dim + rope_dim)
+    return out[..., :nope_dim], out[..., nope_dim:]

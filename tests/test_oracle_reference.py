@@ -353,3 +353,30 @@ def test_flash_sparse_mla_special_cases():
     only5 = ref.flash_sparse_mla(q2[:1], qp2[:1], kv, pe, torch.tensor([[5]]), 30, 0.1)
     assert torch.equal(two[0], only5[0])
     assert not torch.equal(two[1], ref.flash_sparse_mla(q2[1:], qp2[1:], kv, pe, torch.tensor([[5]]), 30, 0.1)[0])
+
+
+# ------------------------------------------------------- q RMSNorm + wq_b (BF16MMA)
+def test_rmsnorm_projq_wqb_vs_fp64_and_head_split():
+    g = synth.gen(51)
+    s, heads, rank = 4, 4, 256
+    q = (torch.randn(s, rank, generator=g) * 2).to(torch.bfloat16)
+    gamma = torch.rand(rank, generator=g) + 0.5
+    wq, ws = ref.weight_quant(synth.weight_fp32(heads * 192, rank, g))
+    nope, pe = ref.rmsnorm_projq_wqb(q, gamma, wq, ws, heads)
+    assert nope.shape == (s, heads, 128) and pe.shape == (s, heads, 64)
+    # fp64: the norm (rounded to bf16, as the golden), the weight's bf16 dequantisation
+    qd = q.double()
+    qr = (qd * torch.rsqrt(qd.pow(2).mean(-1, keepdim=True) + 1e-6) * gamma.double()).to(torch.bfloat16).double()
+    wd = (wq.float() * ws.repeat_interleave(128, 0).repeat_interleave(128, 1)).to(torch.bfloat16).double()
+    want = (qr @ wd.T).view(s, heads, 192)
+    got = torch.cat([nope, pe], -1).double()
+    assert ((got - want).norm() / want.norm()).item() < 4e-3
+    # head h's rows 192 h .. 192 h + 127 are its nope part, the next 64 its rope part
+    assert torch.equal(torch.cat([nope, pe], -1).reshape(s, heads * 192), torch.cat(
+        [torch.cat([nope[:, h], pe[:, h]], -1) for h in range(heads)], -1))
+    # a one-hot weight row picks one normalised input element
+    wq1 = torch.zeros(heads * 192, rank)
+    wq1[5, 17] = 1.0
+    q1, s1 = ref.weight_quant(wq1)
+    n1, _ = ref.rmsnorm_projq_wqb(q, gamma, q1, s1, heads)
+    assert torch.equal(n1[:, 0, 5].float(), (qr[:, 17].float() * wd.new_tensor(1.0).float()).to(torch.bfloat16).float())

@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "tl_flash_sparse_mla": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, ctypes.c_float, _c_void_p, _c_void_p,
                                    _c_void_p, _c_void_p, _c_void_p]),
+    "tl_rmsnorm_projq_wqb": (_int, [_c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _c_void_p,
+                                    _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
     "tl_topk_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "tl_topk_rows": (_int, [_c_void_p, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _size,
                             _c_void_p]),

@@ -77,6 +77,25 @@ __device__ inline float group_scale(float amax, int scale_mode) {
   return amax * (1.0f / 448.0f);
 }
 
+// ---------------------------------------------------------- bf16 dequantisation
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+__device__ inline uint32_t bf16x2_bits(v2f f) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));  // v_cvt_pk_bf16_f32, RNE
+}
+
+// fp8 dwords d0, d1 (8 weights, k order = byte order) -> bf16(fp32(q) * s) MFMA operand.
+__device__ inline v8bf dequant8_bf16(uint32_t d0, uint32_t d1, float s) {
+  uint32_t __attribute__((ext_vector_type(4))) r;
+  r.x = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, false) * s);
+  r.y = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, true) * s);
+  r.z = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, false) * s);
+  r.w = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, true) * s);
+  return __builtin_bit_cast(v8bf, r);
+}
+
 // --------------------------------------------------------------- MFMA tile helper
 // One wave: C[16x16] = A[16x128] * B[128x16] in fp8 with fp32 accumulation.
 //

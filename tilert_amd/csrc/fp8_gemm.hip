@@ -1012,6 +1012,116 @@ static int validate(const char* who, const void* a, const float* a_s, const void
   return kOk;
 }
 
+// ------------------------------------------------ q RMSNorm + wq_b on bf16 MFMA
+// RmsnormProjqWqb (rmsnorm_projq_wqb.py:20-44, golden :496-512): qr = bf16(rms_norm(q) *
+// weight) in fp32, then qr . dequant(wq_b)^T with the weight dequantised to bf16(fp32(w8) *
+// scale) (the golden's bf16 ref_wq_b) on v_mfma_f32_16x16x32_bf16 with fp32 accumulation,
+// written per head as q_nope [M, heads, nope] and q_pe [M, heads, rope].  One launch: every
+// workgroup recomputes the M <= 16 normalised rows (wave w normalises rows w, w+4, ...)
+// into LDS as bf16 -- a few KB from L2 -- then its 4 waves stream the packed weight
+// fragments of one 16-row tile (K blocks w, w+4, ...), all loads issued up front.
+constexpr int kPqWaves = 4;
+constexpr int kPqMaxKb = 16;  // K <= 2048: at most 4 K blocks per wave
+
+__global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
+    const uint16_t* __restrict__ q, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, uint16_t* __restrict__ q_nope, uint16_t* __restrict__ q_pe, int M, int N, int K,
+    int nope, int rope) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];  // [M][K] normalised bf16 rows
+  __shared__ float red[kPqWaves - 1][4][64];
+  constexpr int KPW = kPqMaxKb / kPqWaves;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int KB = K >> 7, NT = N >> 4, t = blockIdx.x;
+  // this wave's weight fragments and scales first (unconditional; blocks past K weigh 0)
+  v8i wf[KPW];
+  float ws[KPW];
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int kb = min(wave + i * kPqWaves, KB - 1);
+    wf[i] = load_packed_fragment(B + packed_fragment(t, kb, NT), lane);
+    ws[i] = wave + i * kPqWaves < KB ? Bs[static_cast<size_t>((16 * t) >> 7) * KB + kb] : 0.f;
+  }
+  // normalised rows: x * rsqrt(mean(x^2) + eps) * gamma in fp32, rounded to bf16.  Lane l
+  // holds elements 8 l + 512 i .. +7 (16-byte loads, all issued together; chunks past K
+  // reload chunk 0 and are not used)
+  constexpr int CPL = kPqMaxKb * kBlock / 512;  // chunks per lane
+  typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+  const int nch = K >> 9;
+  for (int m = wave; m < M; m += kPqWaves) {
+    const uint16_t* row = q + static_cast<size_t>(m) * K;
+    u32x4q xv[CPL];
+    v4f g0[CPL], g1[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int k0 = i < nch ? 512 * i + 8 * lane : 8 * lane;
+      xv[i] = *reinterpret_cast<const u32x4q*>(row + k0);
+      g0[i] = *reinterpret_cast<const v4f*>(gamma + k0);
+      g1[i] = *reinterpret_cast<const v4f*>(gamma + k0 + 4);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if (i < nch) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16_to_f32(xv[i][e] & 0xffffu), hi = bf16_to_f32(xv[i][e] >> 16);
+          ss += lo * lo + hi * hi;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float rs = 1.0f / sqrtf(ss / static_cast<float>(K) + eps);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      if (i < nch) {
+        u32x4q o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float ga = e < 2 ? g0[i][2 * e] : g1[i][2 * e - 4], gb = e < 2 ? g0[i][2 * e + 1] : g1[i][2 * e - 3];
+          o[e] = f32_to_bf16(bf16_to_f32(xv[i][e] & 0xffffu) * rs * ga) |
+                 (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(xv[i][e] >> 16) * rs * gb)) << 16);
+        }
+        *reinterpret_cast<u32x4q*>(xl + m * K + 512 * i + 8 * lane) = o;
+      }
+    }
+  }
+  __syncthreads();
+  // 16 weight rows x 16 tokens (rows past M repeat row M-1 and are not stored)
+  const uint16_t* xrow = xl + min(r, M - 1) * K;
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int kb = min(wave + i * kPqWaves, KB - 1);
+    const uint16_t* xk = xrow + kb * kBlock;
+    const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const v8bf xa = *reinterpret_cast<const v8bf*>(xk + off[j]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(wf[i][2 * j], wf[i][2 * j + 1], ws[i]), xa, acc, 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wave - 1][j][lane] = acc[j];
+  }
+  __syncthreads();
+  if (wave != 0 || r >= M) return;
+#pragma unroll
+  for (int w = 0; w < kPqWaves - 1; ++w)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] += red[w][j][lane];
+  // features f .. f+3 of token r: head f / (nope + rope), inside one 16-wide tile
+  const int f = 16 * t + 4 * g, hd = nope + rope;
+  const int head = f / hd, d = f % hd;
+  const int heads = N / hd;
+  uint16_t* dst = d < nope ? q_nope + (static_cast<size_t>(r) * heads + head) * nope + d
+                           : q_pe + (static_cast<size_t>(r) * heads + head) * rope + (d - nope);
+  *reinterpret_cast<uint2*>(dst) = pack_bf16x4(acc);
+}
+
 }  // namespace tl
 
 using namespace tl;
@@ -1099,4 +1209,32 @@ extern "C" int tl_projx_wqkva(const void* x_q, const float* x_s, const void* w_p
                (int)q_rank, (int)kv_rank, (int)rope_dim, cur_pos, (int)seq, (int)cache_rows};
   return launch_gemm<true>((const uint8_t*)x_q, x_s, (const uint8_t*)w_packed, w_s, out, (int)M, (int)N,
                            (int)dim, workspace, (hipStream_t)stream);
+}
+
+extern "C" int tl_rmsnorm_projq_wqb(const void* q_bf16, const float* q_norm_weight, float eps, const void* wq_b_packed,
+                                    const float* wq_b_s, void* q_nope_bf16, void* q_pe_bf16, int64_t M, int64_t heads,
+                                    int64_t q_rank, int64_t nope_dim, int64_t rope_dim, void* stream) {
+  const int64_t N = heads * (nope_dim + rope_dim), K = q_rank;
+  if (M < 1 || M > 16) { set_error("rmsnorm_projq_wqb: M=%lld must be in [1, 16]", (long long)M); return kErrUnsupported; }
+  if (heads < 1 || nope_dim <= 0 || rope_dim <= 0 || nope_dim % 16 || rope_dim % 16) {
+    set_error("rmsnorm_projq_wqb: heads=%lld, nope=%lld, rope=%lld (dims must be positive multiples of 16)",
+              (long long)heads, (long long)nope_dim, (long long)rope_dim);
+    return kErrArg;
+  }
+  if (K % (kBlock * kGroup) || K > kPqMaxKb * kBlock) { set_error("rmsnorm_projq_wqb: q_rank=%lld must be a multiple of 512 and <= %d", (long long)K, kPqMaxKb * kBlock); return kErrUnsupported; }
+  if (!q_bf16 || !q_norm_weight || !wq_b_packed || !wq_b_s || !q_nope_bf16 || !q_pe_bf16) { set_error("rmsnorm_projq_wqb: null pointer"); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(q_bf16) | reinterpret_cast<uintptr_t>(wq_b_packed)) & 15 ||
+      (reinterpret_cast<uintptr_t>(q_nope_bf16) | reinterpret_cast<uintptr_t>(q_pe_bf16)) & 7) {
+    set_error("rmsnorm_projq_wqb: q and the weight must be 16-byte aligned, outputs 8-byte aligned");
+    return kErrArg;
+  }
+  const size_t lds = static_cast<size_t>(M) * K * 2;
+  if (lds > 48 * 1024) {
+    if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(rmsnorm_projq_kernel), static_cast<int>(lds), "rmsnorm_projq_wqb"))
+      return rc;
+  }
+  hipLaunchKernelGGL(rmsnorm_projq_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kPqWaves * 64), lds, (hipStream_t)stream,
+                     (const uint16_t*)q_bf16, q_norm_weight, eps, (const uint8_t*)wq_b_packed, wq_b_s, (uint16_t*)q_nope_bf16,
+                     (uint16_t*)q_pe_bf16, (int)M, (int)N, (int)K, (int)nope_dim, (int)rope_dim);
+  return check_launch("rmsnorm_projq_wqb");
 }

@@ -27,8 +27,6 @@
 
 namespace tl {
 
-typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups per CU)
@@ -37,22 +35,6 @@ constexpr int kDownSlots = 4;  // hit experts reduced together by the down kerne
 constexpr int kDownRedBytes = sizeof(float) * kDownWaves * kDownSlots * 4 * 64;  // cross-wave partials
 constexpr int kDownTermBytes = sizeof(float) * kDownSlots * 4 * 64;              // per-slot terms
 constexpr int kMaxLocalExperts = 64;
-
-typedef float v2f __attribute__((ext_vector_type(2)));
-
-__device__ inline uint32_t bf16x2_bits(v2f f) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, v2bf));  // v_cvt_pk_bf16_f32, RNE
-}
-
-// fp8 dwords d0, d1 (8 weights, k order = byte order) -> bf16(fp32(q) * s) MFMA operand.
-__device__ inline v8bf dequant8_bf16(uint32_t d0, uint32_t d1, float s) {
-  u32x4 r;
-  r.x = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, false) * s);
-  r.y = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d0, true) * s);
-  r.z = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, false) * s);
-  r.w = bf16x2_bits(__builtin_amdgcn_cvt_pk_f32_fp8(d1, true) * s);
-  return __builtin_bit_cast(v8bf, r);
-}
 
 __device__ inline v8i load_fragment(const uint8_t* frag, int lane) {
   const u32x4* p = reinterpret_cast<const u32x4*>(frag);
