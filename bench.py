@@ -138,6 +138,18 @@ def cpu_model() -> str:
 
 
 # ----------------------------------------------------------------------------- extras
+def _cpu_time_us(torch, fn, reps=3):
+    """Median wall time of fn() on the host cores (after one warm-up call)."""
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter_ns()
+        fn()
+        ts.append((time.perf_counter_ns() - t0) / 1e3)
+    return round(statistics.median(ts), 1)
+
+
 def extras(torch, steps, dev):
     from tilert_amd import moe, sparse_index as si
     from tilert_amd.topk import topk_rows
@@ -161,8 +173,12 @@ def extras(torch, steps, dev):
     mla = {"wq_a": (7168, 1536), "wq_b": (1536, 3072), "wkv_a": (7168, 576), "wkv_b": (512, 4096), "wo": (2048, 7168)}
     tot_us, tot_b = 0.0, 0
     per = {}
+    from oracle import reference as ref  # the checker/baseline only
+    cpu_layers = []
     for name, (K, N) in mla.items():
-        us, *_ = bench_gemm(torch, 4, N, K, st, 5, 8, dev, seed=len(name))
+        us, ws_, _x, xq_, xs_q, _o = bench_gemm(torch, 4, N, K, st, 5, 8, dev, seed=len(name))
+        cpu_layers.append((ref.act_dequant(xq_.cpu(), xs_q.cpu()), ref.weight_dequant(ws_[0][0].cpu(), ws_[0][1].cpu())))
+        del ws_
         b = gemm_bytes(4, N, K)
         per[name] = {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)}
         tot_us += us
@@ -209,7 +225,12 @@ def extras(torch, steps, dev):
     b_pq = 3072 * 1536 + 24 * 12 * 4 + 4 * 1536 * 2 + 1536 * 4 + 4 * 3072 * 2
     pq = {"us": round(us_pq, 2), "GBs": round(b_pq / us_pq / 1e3, 1),
           "rmsnorm_quant_then_fp8_gemv_us": round(us_pq2, 2)}
+    # the reference torch path on the host cores: the goldens' fp32 x_deq @ W_deq^T -> bf16,
+    # weights dequantised beforehand (as init_reference_weights does)
+    mla_cpu = _cpu_time_us(torch, lambda: [(xd @ wd.T).to(torch.bfloat16) for xd, wd in cpu_layers])
+    del cpu_layers
     out["mla_projections_M4"] = {"layers": per, "us_total": round(tot_us, 2),
+                                 "cpu_baseline_us": mla_cpu, "cpu_threads": len(os.sched_getaffinity(0)),
                                  "GBs": round(tot_b / tot_us / 1e3, 1),
                                  "hbm_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 3),
                                  "projx_wqkva": {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)},
@@ -248,6 +269,8 @@ def extras(torch, steps, dev):
                 ss_.append(s)
             parts += [torch.stack(qs_), torch.stack(ss_)]
         copies.append(moe.LocalExperts(*parts, expert_begin=32))
+        if len(copies) == 1:
+            moe_parts0 = parts
         del parts, qs_, ss_
     gc = torch.Generator().manual_seed(3)
     routes = []
@@ -263,8 +286,30 @@ def extras(torch, steps, dev):
     mean_hits = sum(r[2] for r in routes) / len(routes)
     per_expert = 3 * I * D + 3 * (I // 128) * (D // 128) * 4
     b = mean_hits * per_expert + M * D * 2 * 2 + mean_hits * M * I * 2 * 2
+    # the reference torch path on the host cores for routes[0]: the goldens' per-pair fp32
+    # products with bf16-rounded dequantised weights (expert_sel_up_gate_silu.py:670-692,
+    # expert_down_allreduce.py:455-468), weights of the hit experts dequantised beforehand
+    idx0, w0 = routes[0][0].cpu(), routes[0][1].cpu()
+    hit0 = ref.hit_experts(idx0, 32, E)
+    deq = {}
+    for e in hit0:
+        deq[e] = [ref.weight_dequant(moe_parts0[2 * j][e].cpu(), moe_parts0[2 * j + 1][e].cpu()).to(torch.bfloat16).float()
+                  for j in range(3)]
+    xc = x.cpu().float()
+
+    def moe_cpu():
+        y_ = torch.zeros(M, D)
+        for (t, kk, e) in ref.local_pairs(idx0, 32, E):
+            g_, u_, d_ = deq[e]
+            hh = (torch.nn.functional.silu(xc[t] @ g_.T) * (xc[t] @ u_.T)).to(torch.bfloat16).float()
+            y_[t] += (w0[t, kk] * (hh @ d_.T)).to(torch.bfloat16).float()
+        return y_.to(torch.bfloat16)
+    moe_cpu_us = _cpu_time_us(torch, moe_cpu)
+    del deq, moe_parts0
     out["moe_ep8_M4"] = {"us": round(us, 2), "mean_hit_experts": mean_hits, "GBs": round(b / us / 1e3, 1),
-                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3)}
+                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3),
+                         "cpu_baseline_us": moe_cpu_us, "cpu_baseline_hit_experts": len(hit0),
+                         "cpu_threads": len(os.sched_getaffinity(0))}
     del copies
 
     # config 4: indexer + top-2048 at 128K
@@ -287,7 +332,22 @@ def extras(torch, steps, dev):
     us_k = _graph_time_us(torch, lambda i: topk_rows(logits, L - 4, k, out=idx), st, 5)
     b_s = L * 128 + L * 4 + M * H * 128 + M * 4 + M * H * 2 + M * L * 4
     flops = 2 * M * H * 128 * L
+    # the reference torch path on the host cores: fp32 einsum of the dequantised q and keys,
+    # ReLU, head-weighted sum, causal mask, torch.topk (ops/topk.py:128-143)
+    qd_c = (q.float() * qsc[:, None, None]).cpu()
+    kd_c = (caches[0][0].float() * caches[0][1][:, None]).cpu()
+    w_c = w.float().cpu()
+
+    def idx_cpu():
+        sc_ = torch.einsum("thd,ld->thl", qd_c, kd_c).relu_()
+        lg = torch.einsum("thl,th->tl", sc_, w_c)
+        lim = (L - 4 + torch.arange(M))[:, None]
+        lg = torch.where(torch.arange(L)[None, :] <= lim, lg, torch.tensor(float("-inf")))
+        return lg.topk(k, dim=-1).indices
+    idx_cpu_us = _cpu_time_us(torch, idx_cpu)
+    del qd_c, kd_c
     out["indexer_128k_M4"] = {"scores_us": round(us_s, 2), "topk_us": round(us_k, 2),
+                              "cpu_baseline_us": idx_cpu_us, "cpu_threads": len(os.sched_getaffinity(0)),
                               "scores_GBs": round(b_s / us_s / 1e3, 1),
                               "scores_hbm_frac": round(b_s / us_s / 1e3 / HBM_PEAK_GBS, 3),
                               "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 3),
