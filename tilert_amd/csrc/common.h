@@ -159,13 +159,19 @@ typedef __attribute__((address_space(3))) uint8_t* lds_u8_ptr;
 // compiler cannot tell these LDS writes from the operand reads of another ring stage and
 // puts a wait for every copy in flight before each LDS read; as assembly they are
 // invisible to it, and the kernel's own s_waitcnt + s_barrier order them.
+// m0 is saved into a scratch SGPR and restored inside the statement: it is a reserved
+// register that the compiler may keep live, so the assembly leaves it as it found it.
 __device__ inline void copy_to_lds16(const void* src, uint8_t* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(m0) : "memory");
 }
 __device__ inline void copy_to_lds4(const void* src, uint8_t* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)lds)));
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(m0) : "memory");
 }
 
 // Software pipeline over n items with D operand buffers: item i's loads are issued D-1

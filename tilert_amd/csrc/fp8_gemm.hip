@@ -381,7 +381,6 @@ __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
 
 constexpr int kTiledWaves = 8;
 constexpr int kTiledDepth = 4;
-constexpr int kTiledChunkBytes = 32 * 1024;
 
 template <int TT>
 struct TiledShape {
