@@ -200,6 +200,14 @@ def extras(torch, steps, dev):
                                                      model_arch="deepseek_v3_2"), st, 5)
     b = gemm_bytes(4, 2112, 7168)
     fused_us = tot_us - per["wq_a"]["us"] - per["wkv_a"]["us"] + us
+    # the DECOUPLED RMSNormProjxWqkva: rmsnorm_quant then projx_wqkva
+    from tilert_amd.projx import rmsnorm_projx_wqkva
+    xb4 = [torch.randn(1, 4, 7168, device=dev).to(torch.bfloat16) for _ in range(4)]
+    gx = torch.rand(7168, device=dev) + 0.5
+    us_rx = _graph_time_us(torch, lambda i: rmsnorm_projx_wqkva(xb4[i % 4], gx, pw[i % 8], cur4, q4, kv4, pe4,
+                                                                model_arch="deepseek_v3_2"), st, 5)
+    b_rx = gemm_bytes(4, 2112, 7168) - 4 * 7168 - 4 * 56 * 4 + 4 * 7168 * 2 + 7168 * 4
+    rx = {"us": round(us_rx, 2), "GBs": round(b_rx / us_rx / 1e3, 1), "launches": 2}
     # q RMSNorm + wq_b in one launch (RmsnormProjqWqb, BF16MMA) against RMSNorm + act_quant
     # followed by the FP8 GEMV
     from tilert_amd.rmsnorm_projq_wqb import rmsnorm_projq_wqb_op
@@ -235,6 +243,7 @@ def extras(torch, steps, dev):
                                  "hbm_frac": round(tot_b / tot_us / 1e3 / HBM_PEAK_GBS, 3),
                                  "projx_wqkva": {"us": round(us, 2), "GBs": round(b / us / 1e3, 1)},
                                  "rmsnorm_projq_wqb": pq,
+                                 "rmsnorm_projx_wqkva": rx,
                                  "us_total_with_projx": round(fused_us, 2),
                                  "hbm_frac_with_projx": round(tot_b / fused_us / 1e3 / HBM_PEAK_GBS, 3)}
 

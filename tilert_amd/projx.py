@@ -99,3 +99,30 @@ def projx_wqkva(x_quant: torch.Tensor, x_scale: torch.Tensor, wqkva: PackedWqkva
               wqkva.scale.data_ptr(), cur_pos.data_ptr(), q_out.data_ptr(), kv_out.data_ptr(),
               pe_cache_out.data_ptr(), batch, seq, pe_cache_out.shape[1], dim, q_rank, kv_rank, rope,
               ws_ptr, ws_len, st)
+
+
+
+def rmsnorm_projx_wqkva(x: torch.Tensor, gamma: torch.Tensor, wqkva: PackedWqkva, cur_pos: torch.Tensor,
+                        q_out: torch.Tensor, kv_out: torch.Tensor, pe_cache_out: torch.Tensor,
+                        x_rmsnorm_out: torch.Tensor | None = None, profile_logs: torch.Tensor | None = None, *,
+                        model_arch: str, scale_fmt: str | None = None, eps: float = 1e-6) -> None:
+    """The DECOUPLED ``RMSNormProjxWqkva`` (rmsnorm_projx_wqkva.py:473-509): ``rmsnorm_quant``
+    (RMSNorm + act_quant, one launch) into scratch tensors, then ``projx_wqkva``.  x bf16
+    [batch, seq, dim]; gamma [dim]; outputs as for ``projx_wqkva``; ``x_rmsnorm_out`` (bf16,
+    x's shape), when given, receives the normalised rows.  A single launch that recomputes
+    the norm in every GEMV workgroup measured slower on MI355X (20.8 vs 11.0 us at M = 4,
+    7168 -> 2112): each of its 132 workgroups quantises all M x 7168 values."""
+    from .rmsnorm import rmsnorm_quant
+    if x.dim() != 3 or x.dtype != torch.bfloat16:
+        raise ValueError("rmsnorm_projx_wqkva: x must be bfloat16 [batch, seq, dim]")
+    if not isinstance(wqkva, PackedWqkva):
+        raise ValueError("rmsnorm_projx_wqkva: wqkva must come from pack_wqkva")
+    batch, seq, dim = x.shape
+    if dim != wqkva.K:
+        raise ValueError(f"rmsnorm_projx_wqkva: x dim {dim} does not match the weight's {wqkva.K}")
+    y = torch.empty_like(x) if x_rmsnorm_out is None else x_rmsnorm_out
+    xq = torch.empty(batch, seq, dim, dtype=torch.float8_e4m3fn, device=x.device)
+    xs = torch.empty(batch, seq, dim // BLOCK, dtype=torch.float32, device=x.device)
+    logs = profile_logs if profile_logs is not None else torch.zeros(1, device=x.device)
+    rmsnorm_quant(x, gamma, y, xq, xs, logs, model_arch=model_arch, scale_fmt=scale_fmt, eps=eps)
+    projx_wqkva(xq, xs, wqkva, cur_pos, q_out, kv_out, pe_cache_out, profile_logs, model_arch=model_arch)
