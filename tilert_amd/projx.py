@@ -102,6 +102,9 @@ def projx_wqkva(x_quant: torch.Tensor, x_scale: torch.Tensor, wqkva: PackedWqkva
 
 
 
+_NO_LOGS: dict = {}
+
+
 def rmsnorm_projx_wqkva(x: torch.Tensor, gamma: torch.Tensor, wqkva: PackedWqkva, cur_pos: torch.Tensor,
                         q_out: torch.Tensor, kv_out: torch.Tensor, pe_cache_out: torch.Tensor,
                         x_rmsnorm_out: torch.Tensor | None = None, profile_logs: torch.Tensor | None = None, *,
@@ -123,6 +126,10 @@ def rmsnorm_projx_wqkva(x: torch.Tensor, gamma: torch.Tensor, wqkva: PackedWqkva
     y = torch.empty_like(x) if x_rmsnorm_out is None else x_rmsnorm_out
     xq = torch.empty(batch, seq, dim, dtype=torch.float8_e4m3fn, device=x.device)
     xs = torch.empty(batch, seq, dim // BLOCK, dtype=torch.float32, device=x.device)
-    logs = profile_logs if profile_logs is not None else torch.zeros(1, device=x.device)
+    logs = profile_logs
+    if logs is None:  # rmsnorm_quant requires the tensor; it is never written
+        logs = _NO_LOGS.get(x.device)
+        if logs is None:
+            logs = _NO_LOGS[x.device] = torch.zeros(1, device=x.device)
     rmsnorm_quant(x, gamma, y, xq, xs, logs, model_arch=model_arch, scale_fmt=scale_fmt, eps=eps)
     projx_wqkva(xq, xs, wqkva, cur_pos, q_out, kv_out, pe_cache_out, profile_logs, model_arch=model_arch)
