@@ -76,6 +76,7 @@ def _assert_topk_set(idx, scores, valid, k, rel_gap=1e-3):
     (2, 65536, 8192, 65534),      # 4 chunks x k = 32768 candidates: the stage-B limit
     (2, 49160, 2048, 49157),      # last chunk holds only 8 valid columns
     (2, 131072, 4096, 131070),    # 4096 < candidates <= 8192: the 32-per-thread selection
+    (2, 4096, 8192, 4094),        # k beyond the row's one chunk: -1 padding up to k
 ])
 def test_topk_rows_vs_oracle(cuda, rows, L, k, base):
     g = synth.gen(rows + L + k)

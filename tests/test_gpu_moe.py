@@ -1,5 +1,7 @@
 """GPU parity of the MoE expert layer against the CPU oracle (the reference's BF16MMA
 goldens): gate/up + SwiGLU per hit expert, down + routing-weighted combine."""
+import functools
+
 import pytest
 import torch
 
@@ -10,6 +12,7 @@ from tilert_amd import moe, synth
 pytestmark = pytest.mark.gpu
 
 
+@functools.lru_cache(maxsize=2)
 def _experts(E, D, I, seed):
     g = synth.gen(seed)
     qs = {}
@@ -21,7 +24,7 @@ def _experts(E, D, I, seed):
 
 def _run(M, E, D, I, topk, n_experts, e0, seed, idx=None, w=None):
     cuda = torch.device("cuda:0")
-    W = _experts(E, D, I, seed)
+    W = _experts(E, D, I, E + D + I)  # shared by the cases of one shape
     g = synth.gen(seed + 1)
     x = synth.activations(M, D, g)
     if idx is None:
@@ -43,12 +46,14 @@ def _run(M, E, D, I, topk, n_experts, e0, seed, idx=None, w=None):
     (4, 8, 512, 256, 8, 32, 8),
     (1, 4, 1024, 512, 8, 16, 4),
     (16, 8, 256, 384, 4, 16, 8),
-    (3, 32, 7168, 2048, 8, 256, 32),  # config 2 shapes (shard 1 of 8)
+    (3, 32, 7168, 2048, 8, 256, 32),  # config 2 shapes (shard 1 of 8), odd M
+    (4, 32, 7168, 2048, 8, 256, 32),  # config 2: M = 4, shard 1 of 8
+    (4, 32, 7168, 2048, 8, 256, 224),  # config 2: M = 4, shard 7 of 8
     (16, 8, 512, 256, 8, 32, 0),  # 128 routed pairs: the kernels without LDS activations
     (8, 4, 7168, 256, 2, 16, 0),  # x [8, 7168] exceeds 64 KB: gate/up without LDS, down with
 ])
 def test_moe_vs_oracle(cuda, M, E, D, I, topk, n_exp, e0):
-    y, ry, hits = _run(M, E, D, I, topk, n_exp, e0, seed=M * 1000 + E + D)
+    y, ry, hits = _run(M, E, D, I, topk, n_exp, e0, seed=M * 1000 + E + D + e0)
     if hits:
         assert_gemm_close(y, ry, "moe output")
     else:

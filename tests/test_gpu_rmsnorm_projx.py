@@ -39,7 +39,7 @@ def _case(cuda, batch, seq, arch, max_len, pos, scale_fmt, seed):
     rmsnorm_quant(xd, gd, y, xq, xs, LOGS, model_arch=arch, scale_fmt=scale_fmt)
     two = outs()
     projx_wqkva(xq, xs, w, cur, *two, LOGS, model_arch=arch)
-    # one launch
+    # the module entry point (the same two launches, behind one call)
     one = outs()
     y1 = torch.empty_like(xd)
     rmsnorm_projx_wqkva(xd, gd, w, cur, *one, y1, LOGS, model_arch=arch, scale_fmt=scale_fmt)
@@ -55,7 +55,7 @@ def _case(cuda, batch, seq, arch, max_len, pos, scale_fmt, seed):
     (1, 1, "glm_5", 32, 5, "div"),
     (3, 3, "glm_5", 16, 2, None),
 ])
-def test_fused_equals_rmsnorm_quant_then_projx(cuda, batch, seq, arch, max_len, pos, scale_fmt):
+def test_module_equals_rmsnorm_quant_then_projx(cuda, batch, seq, arch, max_len, pos, scale_fmt):
     x, gamma, wts, (y, xq, xs, two), (y1, one) = _case(cuda, batch, seq, arch, max_len, pos, scale_fmt,
                                                        900 + batch * 10 + seq)
     assert torch.equal(y1, y), "normalised rows differ from rmsnorm_quant's"

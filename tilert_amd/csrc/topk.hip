@@ -227,8 +227,11 @@ __global__ __launch_bounds__(kTkThreads) void topk_kernel(const float* __restric
   const int n = row_valid(row, valid_base, ld);
   int32_t* o = out + static_cast<int64_t>(row) * k;
   if (n <= k) {  // every valid column, then -1 padding (no barrier: the whole row exits)
+    // chunk c writes columns [c kChunk, (c+1) kChunk); the last chunk also pads up to k
+    // when k exceeds the row's chunk span
     const int base = chunk * kChunk;
-    for (int c = base + static_cast<int>(threadIdx.x); c < base + kChunk && c < k; c += kTkThreads)
+    const int end = chunk == chunks - 1 ? k : min(base + kChunk, k);
+    for (int c = base + static_cast<int>(threadIdx.x); c < end; c += kTkThreads)
       o[c] = c < n ? c : -1;
     return;
   }

@@ -19,7 +19,9 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _require_cuda(name: str, *ts: torch.Tensor) -> None:
+def _require_cuda(name: str, *ts: torch.Tensor | None) -> None:
+    """Every tensor that reaches a kernel must live on the same GPU (None = not passed)."""
+    ts = tuple(t for t in ts if t is not None)
     for t in ts:
         if not t.is_cuda:
             raise ValueError(f"{name}: all tensors must be on a GPU (got {t.device})")
@@ -105,11 +107,17 @@ class _Workspace:
 
     def __init__(self) -> None:
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        # Buffers replaced by a larger one stay allocated until the process ends: a HIP
+        # graph captured while one of them was current still addresses it on replay, so
+        # freeing it would hand its (no longer zeroed) memory to another tensor.
+        self._retired: list[torch.Tensor] = []
 
     def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         key = (device.index, stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
@@ -180,6 +188,7 @@ def fp8_gemm(a: torch.Tensor, a_s: torch.Tensor, b, b_s: torch.Tensor | None = N
         out = a.new_empty(*a.size()[:-1], N, dtype=torch.bfloat16)
     elif out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != M * N:
         raise ValueError("fp8_gemm: out must be a contiguous bf16 tensor of M*N elements")
+    _require_cuda("fp8_gemm", a, out)
     st = _stream(a)
     nbytes = _lib.query("tl_fp8_gemm_workspace_bytes", M, N, K)
     ws_ptr, ws_len = None, 0

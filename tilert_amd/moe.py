@@ -88,12 +88,12 @@ def expert_select_up_gate_silu(hidden_in: torch.Tensor, expert_indices: torch.Te
     x = _tokens(hidden_in, experts.D)
     M = x.shape[0]
     idx = _routing(expert_indices, M)
-    _require_cuda("expert_select_up_gate_silu", x, idx)
     if hidden_out is None:
         hidden_out = torch.empty(experts.n_local, M, experts.I, dtype=torch.bfloat16, device=x.device)
     elif hidden_out.dtype != torch.bfloat16 or hidden_out.numel() < experts.n_local * M * experts.I \
             or not hidden_out.is_contiguous():
         raise ValueError("hidden_out must be a contiguous bf16 tensor of n_local*M*I elements")
+    _require_cuda("expert_select_up_gate_silu", x, idx, experts.w13, experts.s13, hidden_out)
     _lib.call("tl_moe_gate_up_swiglu", x.data_ptr(), experts.w13.data_ptr(), experts.s13.data_ptr(),
               idx.data_ptr(), M, idx.shape[1], experts.expert_begin, experts.n_local, experts.D,
               experts.I, hidden_out.data_ptr(), _stream(x))
@@ -127,11 +127,11 @@ def expert_down_allreduce(vec_in: torch.Tensor, experts: LocalExperts, indices: 
     if vec_in.dtype != torch.bfloat16 or not vec_in.is_contiguous() \
             or vec_in.numel() < experts.n_local * M * experts.I:
         raise ValueError("vec_in must be the contiguous bf16 [n_local, M, I] gate/up output")
-    _require_cuda("expert_down_allreduce", vec_in, idx, w)
     if vec_out is None:
         vec_out = torch.empty(M, experts.D, dtype=torch.bfloat16, device=vec_in.device)
     elif vec_out.dtype != torch.bfloat16 or vec_out.numel() != M * experts.D or not vec_out.is_contiguous():
         raise ValueError("vec_out must be a contiguous bf16 tensor of M*D elements")
+    _require_cuda("expert_down_allreduce", vec_in, idx, w, experts.w2, experts.s2, vec_out)
     _lib.call("tl_moe_down_combine", vec_in.data_ptr(), experts.w2.data_ptr(), experts.s2.data_ptr(),
               idx.data_ptr(), w.data_ptr(), M, idx.shape[1], experts.expert_begin, experts.n_local,
               experts.D, experts.I, vec_out.data_ptr(), _stream(vec_in))

@@ -87,7 +87,7 @@ def projx_wqkva(x_quant: torch.Tensor, x_scale: torch.Tensor, wqkva: PackedWqkva
     for t in (x_quant, x_scale, q_out, kv_out, pe_cache_out, cur_pos):
         if not t.is_contiguous():
             raise ValueError("projx_wqkva: tensors must be contiguous")
-    _require_cuda("projx_wqkva", x_quant, x_scale, wqkva.data, q_out, kv_out, pe_cache_out, cur_pos)
+    _require_cuda("projx_wqkva", x_quant, x_scale, wqkva.data, wqkva.scale, q_out, kv_out, pe_cache_out, cur_pos)
     M, N = batch * seq, wqkva.N
     st = _stream(x_quant)
     nbytes = _lib.query("tl_fp8_gemm_workspace_bytes", M, N, dim)

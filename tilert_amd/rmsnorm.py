@@ -43,8 +43,8 @@ def rmsnorm_quant(hidden_in: torch.Tensor, gamma_in: torch.Tensor, hidden_out: t
     for t in (hidden_in, hidden_out, quant_hidden_out, quant_hidden_scale_out):
         if t is not None and not t.is_contiguous():
             raise ValueError("rmsnorm_quant tensors must be contiguous")
-    _require_cuda("rmsnorm_quant", hidden_in)
     gamma = gamma_in.reshape(dim).to(torch.float32).contiguous()
+    _require_cuda("rmsnorm_quant", hidden_in, gamma, hidden_out, quant_hidden_out, quant_hidden_scale_out)
     rows = hidden_in.numel() // dim if dim else 0
     _lib.call("tl_rmsnorm_quant", hidden_in.data_ptr(), gamma.data_ptr(), float(eps), rows, dim,
               hidden_out.data_ptr(),
