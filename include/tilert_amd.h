@@ -105,6 +105,20 @@ int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, co
                        void* c_bf16, int64_t M, int64_t N, int64_t K, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of tl_fp8_gemm_packed -- NO COUNTERPART IN THE REFERENCE.  For
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same kernels and results (bit for bit), with
+ * their scratch (split-K counters and partials, the activation image) in a static device
+ * array of TL_FP8_GEMM_STATIC_SCRATCH_BYTES that each GPU holds until the process ends,
+ * instead of a workspace argument.  The call allocates nothing; shapes whose scratch would
+ * exceed the maximum fail with status 3 (every dense MLP shape of 7168 <-> 18432 up to
+ * M = 256 fits).  Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or different threads without ordering) race; calls on one stream are
+ * safe.  A device's first call enqueues a small fill kernel that zeroes the counters. */
+#define TL_FP8_GEMM_STATIC_SCRATCH_BYTES (40u << 20)
+int tl_fp8_gemm_packed_static(const void* a, const float* a_s, const void* b_packed, const float* b_s,
+                              void* c_bf16, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* The fused attention down-projection of one decode step: x_q . [wq_a; wkv_a]^T in one
  * launch, its columns routed to three outputs.  x_q fp8 [batch*seq, dim] + x_s fp32
  * [batch*seq, dim/128]; w_packed = tl_fp8_pack_weight of the row-stacked weight

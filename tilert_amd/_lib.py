@@ -33,6 +33,8 @@ SIGNATURES: dict[str, tuple] = {
     "tl_moe_pack_weight": (_int, [_c_void_p, _c_void_p, _i64, _i64, _c_void_p]),
     "tl_fp8_gemm_packed": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                   _i64, _i64, _i64, _c_void_p, _size, _c_void_p]),
+    "tl_fp8_gemm_packed_static": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                         _i64, _i64, _i64, _c_void_p]),
     "tl_projx_wqkva": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                               _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _c_void_p, _size, _c_void_p]),

@@ -27,6 +27,7 @@
 //     in LDS (see below).
 #include <algorithm>
 #include <type_traits>
+#include <mutex>
 #include <utility>
 
 #include "common.h"
@@ -1125,14 +1126,17 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
 
 using namespace tl;
 
+// Workspace bytes of one weight layout's plan (0 = none).
+static size_t plan_workspace_bytes(int64_t M, int64_t N, int64_t K, bool packed) {
+  const GemmPlan p = plan_gemm(M, N, K, packed);
+  if (p.ksplit > 1 || p.xf || p.mm) return image_offset(p, M, N, K) + (p.xf ? act_image_bytes(M, K) : 0);
+  return 0;
+}
+
 extern "C" size_t tl_fp8_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % 16 || K % kBlock || M > 256) return 0;
-  size_t need = 0;
-  for (bool packed : {false, true}) {  // one size serves both weight layouts
-    const GemmPlan p = plan_gemm(M, N, K, packed);
-    if (p.ksplit > 1 || p.xf || p.mm) need = std::max(need, image_offset(p, M, N, K) + (p.xf ? act_image_bytes(M, K) : 0));
-  }
-  return need;
+  // one size serves both weight layouts
+  return std::max(plan_workspace_bytes(M, N, K, false), plan_workspace_bytes(M, N, K, true));
 }
 
 extern "C" int tl_fp8_gemm(const void* a, const float* a_s, const void* b, const float* b_s,
@@ -1236,4 +1240,74 @@ extern "C" int tl_rmsnorm_projq_wqb(const void* q_bf16, const float* q_norm_weig
                      (const uint16_t*)q_bf16, q_norm_weight, eps, (const uint8_t*)wq_b_packed, wq_b_s, (uint16_t*)q_nope_bf16,
                      (uint16_t*)q_pe_bf16, (int)M, (int)N, (int)K, (int)nope_dim, (int)rope_dim);
   return check_launch("rmsnorm_projq_wqb");
+}
+
+// ------------------------------------------ allocation-free entry point (static scratch)
+// tl_fp8_gemm_packed_static runs tl_fp8_gemm_packed's kernels with their scratch (the
+// split-K counters, fp32 partials and the activation image) in a file-scope device array
+// instead of a caller-passed workspace, for callers that cannot allocate device memory.
+// Each GPU holds its own copy of the array for the life of the process.  In host code
+// `scratch` names a host-side stand-in, never the device memory: its per-device address
+// comes from hipGetSymbolAddress (with that device current) and only that address is
+// passed to kernels.
+static_assert(TL_FP8_GEMM_STATIC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) uint8_t scratch[TL_FP8_GEMM_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of each device's `scratch`
+
+__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The current device's scratch address; on a device's first call it is looked up and the
+// counter region (which every call leaves zero again) is cleared with a fill kernel on
+// `st`, ahead of that call's GEMM.
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) { set_error("fp8_gemm_packed_static: hipGetDevice failed: %s", hipGetErrorString(e)); return kErrHip; }
+  if (dev < 0 || dev >= kMaxDevices) { set_error("fp8_gemm_packed_static: device %d out of range", dev); return kErrUnsupported; }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      set_error("fp8_gemm_packed_static: hipGetSymbolAddress failed on device %d: %s", dev, hipGetErrorString(e));
+      return kErrHip;
+    }
+    const int words = static_cast<int>(kCounterBytes / sizeof(uint32_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(cdiv(words, 256)), dim3(256), 0, st, static_cast<uint32_t*>(ptr), words);
+    if (int rc = check_launch("fp8_gemm_packed_static")) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" int tl_fp8_gemm_packed_static(const void* a, const float* a_s, const void* b_packed, const float* b_s,
+                                         void* c_bf16, int64_t M, int64_t N, int64_t K, void* stream) {
+  const char* who = "fp8_gemm_packed_static";
+  if (K % (kBlock * kGroup)) { set_error("%s: K=%lld must be a multiple of 512", who, (long long)K); return kErrArg; }
+  int rc = validate(who, a, a_s, b_packed, b_s, c_bf16, M, N, K, nullptr, 0, 0);
+  if (rc) return rc;
+  const size_t need = plan_workspace_bytes(M, N, K, true);
+  if (need > TL_FP8_GEMM_STATIC_SCRATCH_BYTES) {
+    set_error("%s: M=%lld N=%lld K=%lld needs %zu bytes of scratch, above the static maximum of %zu", who,
+              (long long)M, (long long)N, (long long)K, need, static_cast<size_t>(TL_FP8_GEMM_STATIC_SCRATCH_BYTES));
+    return kErrUnsupported;
+  }
+  void* ws = nullptr;
+  if (need) {
+    rc = scratch_for_current_device((hipStream_t)stream, &ws);
+    if (rc) return rc;
+  }
+  return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, plain_out((uint16_t*)c_bf16, (int)N),
+                           (int)M, (int)N, (int)K, ws, (hipStream_t)stream);
 }
