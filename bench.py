@@ -11,9 +11,11 @@ repeat reads.
 
   python bench.py [--steps K] [--warmup W] [--extras] [--no-cpu-baseline]
 
-``--extras`` adds (outside the JSON contract's required keys, under "extras") the MLA
-projections (config 1), the MoE layer (config 2), the M sweep (config 3) and the
-indexer + top-k at 128K (config 4), the indexer key producer and sparse MLA attention.
+The same line carries, under "configs", the north star's two other targets, each with its
+achieved HBM fraction and a CPU baseline: the MoE layer at the EP=8 share (config 2) and
+the indexer + exact top-2048 at 128K (config 4).  ``--extras`` adds (under "extras") the
+MLA projections (config 1), the M sweep (config 3), the paged indexer, the indexer key
+producer and sparse MLA attention.
 """
 from __future__ import annotations
 
@@ -137,6 +139,156 @@ def cpu_model() -> str:
     return "unknown"
 
 
+# ----------------------------------------------------------------- configs 2 and 4
+def moe_routes(torch, n, M=4, seed=3):
+    """Config 2's routing: per token 8 distinct experts of 256, softmax weights over N(0,1)
+    logits (CPU generator, so every host draws the same routes)."""
+    gc = torch.Generator().manual_seed(seed)
+    routes = []
+    for _ in range(n):
+        idx = torch.stack([torch.randperm(256, generator=gc)[:8] for _ in range(M)]).to(torch.int32)
+        w = torch.softmax(torch.randn(M, 8, generator=gc), -1)
+        routes.append((idx, w))
+    return routes
+
+
+def bench_moe(torch, steps, dev, cpu=True):
+    """Config 2: the MoE layer at the EP=8 share (32 local experts of 256, here experts
+    32..63), M = 4, top-8.  One step = gate/up + SwiGLU and down + weighted combine for one
+    routing; the routings rotate (one per captured call) over two weight copies (> MALL)."""
+    from tilert_amd import moe
+    E, D, I, M, e0 = 32, 7168, 2048, 4, 32
+    st = max(10, steps // 10)
+    g = torch.Generator(device=dev).manual_seed(2)
+    copies, parts0 = [], None
+    for _ in range(2):
+        parts = []
+        for (n, k) in ((I, D), (I, D), (D, I)):
+            qs_, ss_ = [], []
+            for _e in range(E):
+                q, s = K_.weight_quant(torch.randn(n, k, device=dev, generator=g) * 0.02)
+                qs_.append(q)
+                ss_.append(s)
+            parts += [torch.stack(qs_), torch.stack(ss_)]
+        copies.append(moe.LocalExperts(*parts, expert_begin=e0))
+        if parts0 is None:
+            parts0 = parts
+        del parts, qs_, ss_
+    routes = moe_routes(torch, st, M)
+    routes_d = [(i.to(dev), w.to(dev)) for i, w in routes]
+    hits = [len({int(e) for e in i.flatten() if e0 <= int(e) < e0 + E}) for i, _ in routes]
+    x = torch.randn(M, D, device=dev, generator=g).to(torch.bfloat16)
+    h = torch.empty(E, M, I, dtype=torch.bfloat16, device=dev)
+    y = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    us = _graph_time_us(torch, lambda i: moe.moe_forward(x, copies[i % 2], routes_d[i][0], routes_d[i][1], h, y),
+                        st, 5)
+    mean_hits = sum(hits) / len(hits)
+    per_expert = 3 * I * D + 3 * (I // 128) * (D // 128) * 4
+    # weights of the hit experts + x read + y written + h written and read back
+    b = mean_hits * per_expert + M * D * 2 * 2 + mean_hits * M * I * 2 * 2
+    res = {"us": round(us, 2), "mean_hit_experts": round(mean_hits, 3), "bytes_per_call": round(b),
+           "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+           "routings": len(routes), "weight_copies_rotated": 2}
+    del copies
+    if cpu:
+        # the reference torch path on the host cores over the SAME routings the GPU ran (a
+        # bounded sample of them): the goldens' per-pair fp32 products with bf16-rounded
+        # dequantised weights (expert_sel_up_gate_silu.py:670-692, expert_down_allreduce.py:
+        # 455-468), the bf16 weights of every hit expert dequantised beforehand (as
+        # init_reference_weights does) and widened per use, as the goldens do
+        from oracle import reference as ref  # the checker/baseline only
+        sample = routes[:min(len(routes), 8)]
+        need = sorted({e for i, _ in sample for e in ref.hit_experts(i, e0, E)})
+        deq = {e: [ref.weight_dequant(parts0[2 * j][e].cpu(), parts0[2 * j + 1][e].cpu()).to(torch.bfloat16)
+                   for j in range(3)] for e in need}
+        xc = x.cpu()
+
+        def moe_cpu(idx, w):
+            xf = xc.float()
+            y_ = torch.zeros(M, D)
+            for (t, kk, e) in ref.local_pairs(idx, e0, E):
+                g_, u_, d_ = deq[e]
+                hh = (torch.nn.functional.silu(xf[t] @ g_.float().T) * (xf[t] @ u_.float().T)).to(torch.bfloat16)
+                y_[t] += (w[t, kk] * (hh.float() @ d_.float().T)).to(torch.bfloat16).float()
+            return y_.to(torch.bfloat16)
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        moe_cpu(*sample[0])
+        t0 = time.perf_counter_ns()
+        for idx, w in sample:
+            moe_cpu(idx, w)
+        cus = (time.perf_counter_ns() - t0) / 1e3 / len(sample)
+        s_hits = sum(hits[:len(sample)]) / len(sample)
+        res["cpu_baseline"] = {"us": round(cus, 1), "cores": len(os.sched_getaffinity(0)), "kind": "port",
+                               "sample": f"the first {len(sample)} of the GPU's {len(routes)} routings "
+                                         f"({s_hits:.2f} mean hit experts), one call each after a warm-up"}
+        del deq
+    del parts0
+    torch.cuda.empty_cache()
+    return res
+
+
+def indexer_caches(torch, dev, n, L=131072, seed=4):
+    gk = torch.Generator(device=dev).manual_seed(seed)
+    caches = []
+    for _ in range(n):
+        k32 = torch.randn(L, 128, device=dev, generator=gk)
+        ks = (k32.abs().amax(-1).clamp_min(1e-4) / 448.0).float()
+        caches.append(((k32 / ks[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn), ks))
+        del k32
+    return caches, gk
+
+
+def bench_indexer(torch, steps, dev, cpu=True, keep=False):
+    """Config 4: DSA lightning-indexer scores over an fp8 key cache of 128K keys, M = 4
+    tokens x 64 heads, then the exact top-2048 per token.  20 rotating caches (> MALL)."""
+    from tilert_amd import sparse_index as si
+    from tilert_amd.topk import topk_rows
+    M, H, L, k = 4, 64, 131072, 2048
+    st = max(10, steps // 10)
+    caches, gk = indexer_caches(torch, dev, 20, L)
+    q32 = torch.randn(M, H * 128, device=dev, generator=gk)
+    qsc = (q32.abs().amax(-1).clamp_min(1e-4) / 448.0).float()
+    q = (q32 / qsc[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn).reshape(M, H, 128)
+    w = (torch.randn(M, H, device=dev, generator=gk) / 8).to(torch.bfloat16)
+    logits = torch.empty(M, L, device=dev)
+    idx = torch.empty(M, k, dtype=torch.int32, device=dev)
+    us_s = _graph_time_us(torch, lambda i: si.sparse_index(q, qsc, caches[i % 20][0], caches[i % 20][1], w, logits,
+                                                           L - 4), st, 5)
+    us_k = _graph_time_us(torch, lambda i: topk_rows(logits, L - 4, k, out=idx), st, 5)
+    us_b = _graph_time_us(torch, lambda i: si.sparse_index_topk(q, qsc, caches[i % 20][0], caches[i % 20][1], w,
+                                                                logits, idx, L - 4), st, 5)
+    b_s = L * 128 + L * 4 + M * H * 128 + M * 4 + M * H * 2 + M * L * 4
+    b_all = b_s + M * L * 4 + M * k * 4  # + logits read back by top-k, indices written
+    flops = 2 * M * H * 128 * L
+    res = {"us": round(us_b, 2), "scores_us": round(us_s, 2), "topk_us": round(us_k, 2),
+           "bytes_per_call": b_all, "GBs": round(b_all / us_b / 1e3, 1),
+           "hbm_frac": round(b_all / us_b / 1e3 / HBM_PEAK_GBS, 4),
+           "scores_hbm_frac": round(b_s / us_s / 1e3 / HBM_PEAK_GBS, 4),
+           "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 4), "caches_rotated": 20}
+    if cpu:
+        # the reference torch path on the host cores: fp32 einsum of the dequantised q and
+        # keys, ReLU, head-weighted sum, causal mask, torch.topk (ops/topk.py:128-143)
+        qd_c = (q.float() * qsc[:, None, None]).cpu()
+        kd_c = (caches[0][0].float() * caches[0][1][:, None]).cpu()
+        w_c = w.float().cpu()
+
+        def idx_cpu():
+            sc_ = torch.einsum("thd,ld->thl", qd_c, kd_c).relu_()
+            lg = torch.einsum("thl,th->tl", sc_, w_c)
+            lim = (L - 4 + torch.arange(M))[:, None]
+            lg = torch.where(torch.arange(L)[None, :] <= lim, lg, torch.tensor(float("-inf")))
+            return lg.topk(k, dim=-1).indices
+        res["cpu_baseline"] = {"us": _cpu_time_us(torch, idx_cpu), "cores": len(os.sched_getaffinity(0)),
+                               "kind": "port", "sample": "the full workload on one of the 20 caches, median of 3 "
+                                                         "after a warm-up"}
+        del qd_c, kd_c
+    if keep:
+        return res, caches, q, qsc, w, logits
+    del caches
+    torch.cuda.empty_cache()
+    return res
+
+
 # ----------------------------------------------------------------------------- extras
 def _cpu_time_us(torch, fn, reps=3):
     """Median wall time of fn() on the host cores (after one warm-up call)."""
@@ -151,8 +303,7 @@ def _cpu_time_us(torch, fn, reps=3):
 
 
 def extras(torch, steps, dev):
-    from tilert_amd import moe, sparse_index as si
-    from tilert_amd.topk import topk_rows
+    from tilert_amd import sparse_index as si
     out = {}
     st = max(10, steps // 10)
 
@@ -264,104 +415,15 @@ def extras(torch, steps, dev):
         del ws
     out["m_sweep"] = sweep
 
-    # config 2: MoE at the EP=8 share (32 local experts of 256), M = 4, top-8
-    E, D, I, M = 32, 7168, 2048, 4
-    g = torch.Generator(device=dev).manual_seed(2)
-    copies = []
-    for _ in range(2):
-        parts = []
-        for (n, k) in ((I, D), (I, D), (D, I)):
-            qs_, ss_ = [], []
-            for _e in range(E):
-                q, s = K_.weight_quant(torch.randn(n, k, device=dev, generator=g) * 0.02)
-                qs_.append(q)
-                ss_.append(s)
-            parts += [torch.stack(qs_), torch.stack(ss_)]
-        copies.append(moe.LocalExperts(*parts, expert_begin=32))
-        if len(copies) == 1:
-            moe_parts0 = parts
-        del parts, qs_, ss_
-    gc = torch.Generator().manual_seed(3)
-    routes = []
-    for i in range(st):
-        idx = torch.stack([torch.randperm(256, generator=gc)[:8] for _ in range(M)]).to(torch.int32)
-        w = torch.softmax(torch.randn(M, 8, generator=gc), -1)
-        hits = len({int(e) for e in idx.flatten() if 32 <= int(e) < 64})
-        routes.append((idx.to(dev), w.to(dev), hits))
-    x = torch.randn(M, D, device=dev, generator=g).to(torch.bfloat16)
-    h = torch.empty(E, M, I, dtype=torch.bfloat16, device=dev)
-    y = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
-    us = _graph_time_us(torch, lambda i: moe.moe_forward(x, copies[i % 2], routes[i][0], routes[i][1], h, y), st, 5)
-    mean_hits = sum(r[2] for r in routes) / len(routes)
-    per_expert = 3 * I * D + 3 * (I // 128) * (D // 128) * 4
-    b = mean_hits * per_expert + M * D * 2 * 2 + mean_hits * M * I * 2 * 2
-    # the reference torch path on the host cores for routes[0]: the goldens' per-pair fp32
-    # products with bf16-rounded dequantised weights (expert_sel_up_gate_silu.py:670-692,
-    # expert_down_allreduce.py:455-468), weights of the hit experts dequantised beforehand
-    idx0, w0 = routes[0][0].cpu(), routes[0][1].cpu()
-    hit0 = ref.hit_experts(idx0, 32, E)
-    deq = {}
-    for e in hit0:
-        deq[e] = [ref.weight_dequant(moe_parts0[2 * j][e].cpu(), moe_parts0[2 * j + 1][e].cpu()).to(torch.bfloat16).float()
-                  for j in range(3)]
-    xc = x.cpu().float()
-
-    def moe_cpu():
-        y_ = torch.zeros(M, D)
-        for (t, kk, e) in ref.local_pairs(idx0, 32, E):
-            g_, u_, d_ = deq[e]
-            hh = (torch.nn.functional.silu(xc[t] @ g_.T) * (xc[t] @ u_.T)).to(torch.bfloat16).float()
-            y_[t] += (w0[t, kk] * (hh @ d_.T)).to(torch.bfloat16).float()
-        return y_.to(torch.bfloat16)
-    moe_cpu_us = _cpu_time_us(torch, moe_cpu)
-    del deq, moe_parts0
-    out["moe_ep8_M4"] = {"us": round(us, 2), "mean_hit_experts": mean_hits, "GBs": round(b / us / 1e3, 1),
-                         "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 3),
-                         "cpu_baseline_us": moe_cpu_us, "cpu_baseline_hit_experts": len(hit0),
-                         "cpu_threads": len(os.sched_getaffinity(0))}
-    del copies
-
-    # config 4: indexer + top-2048 at 128K
-    M, H, L, k = 4, 64, 131072, 2048
-    gk = torch.Generator(device=dev).manual_seed(4)
-    caches = []
-    for _ in range(20):  # 20 x 17 MB > 256 MB MALL
-        k32 = torch.randn(L, 128, device=dev, generator=gk)
-        amax = k32.abs().amax(-1).clamp_min(1e-4)
-        ks = (amax / 448.0).float()
-        caches.append(((k32 / ks[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn), ks))
-        del k32
+    # configs 2 and 4 are part of the default line; here the paged form of config 4
+    M, H, L = 4, 64, 131072
+    caches, gk = indexer_caches(torch, dev, 20, L)
     q32 = torch.randn(M, H * 128, device=dev, generator=gk)
     qsc = (q32.abs().amax(-1).clamp_min(1e-4) / 448.0).float()
     q = (q32 / qsc[:, None]).clamp(-448, 448).to(torch.float8_e4m3fn).reshape(M, H, 128)
     w = (torch.randn(M, H, device=dev, generator=gk) / 8).to(torch.bfloat16)
     logits = torch.empty(M, L, device=dev)
-    idx = torch.empty(M, k, dtype=torch.int32, device=dev)
-    us_s = _graph_time_us(torch, lambda i: si.sparse_index(q, qsc, caches[i % 20][0], caches[i % 20][1], w, logits, L - 4), st, 5)
-    us_k = _graph_time_us(torch, lambda i: topk_rows(logits, L - 4, k, out=idx), st, 5)
     b_s = L * 128 + L * 4 + M * H * 128 + M * 4 + M * H * 2 + M * L * 4
-    flops = 2 * M * H * 128 * L
-    # the reference torch path on the host cores: fp32 einsum of the dequantised q and keys,
-    # ReLU, head-weighted sum, causal mask, torch.topk (ops/topk.py:128-143)
-    qd_c = (q.float() * qsc[:, None, None]).cpu()
-    kd_c = (caches[0][0].float() * caches[0][1][:, None]).cpu()
-    w_c = w.float().cpu()
-
-    def idx_cpu():
-        sc_ = torch.einsum("thd,ld->thl", qd_c, kd_c).relu_()
-        lg = torch.einsum("thl,th->tl", sc_, w_c)
-        lim = (L - 4 + torch.arange(M))[:, None]
-        lg = torch.where(torch.arange(L)[None, :] <= lim, lg, torch.tensor(float("-inf")))
-        return lg.topk(k, dim=-1).indices
-    idx_cpu_us = _cpu_time_us(torch, idx_cpu)
-    del qd_c, kd_c
-    out["indexer_128k_M4"] = {"scores_us": round(us_s, 2), "topk_us": round(us_k, 2),
-                              "cpu_baseline_us": idx_cpu_us, "cpu_threads": len(os.sched_getaffinity(0)),
-                              "scores_GBs": round(b_s / us_s / 1e3, 1),
-                              "scores_hbm_frac": round(b_s / us_s / 1e3 / HBM_PEAK_GBS, 3),
-                              "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 3),
-                              "total_us": round(us_s + us_k, 2),
-                              "total_hbm_frac": round((b_s + M * L * 4 + M * k * 4) / (us_s + us_k) / 1e3 / HBM_PEAK_GBS, 3)}
     # the same scores over the KI page layout (64-key pages of 8448 B), 20 rotating page sets
     pages = [si.ki_pages_from_flat(kc, ksc) for kc, ksc in caches]
     del caches
@@ -482,8 +544,12 @@ def main() -> int:
                                "sample": f"full workload, 1 call: torch CPU fp32 x_deq @ W_deq^T -> bf16 with "
                                          f"the weight pre-dequantised (oracle.reference), median of 10 after 3 "
                                          f"warm-up, {cores} threads on {cpu_model()}"}
+    del ws
+    torch.cuda.empty_cache()
+    # configs 2 and 4 (the north star's other two targets) on every default run
+    res["configs"] = {"moe_ep8_M4": bench_moe(torch, args.steps, dev, cpu=not args.no_cpu_baseline),
+                      "indexer_topk_128k_M4": bench_indexer(torch, args.steps, dev, cpu=not args.no_cpu_baseline)}
     if args.extras:
-        del ws
         torch.cuda.empty_cache()
         res["extras"] = extras(torch, args.steps, dev)
     print(json.dumps(res))
