@@ -24,6 +24,14 @@
  *   tl_rmsnorm_projq_wqb  rmsnorm_proj_qb_op  .../ops/rmsnorm_projq_wqb.py:20-44 (golden :496-512)
  *   tl_moe_gate_up_swiglu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_moe_down_combine    expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
+ *                          (these two: config 2's expert-parallel shard, routing as input)
+ *   tl_moe_route           routing of expert_select_up_gate_silu_op (golden _ref_expert_select_ds,
+ *                          glm_5/_dsa_v32/ops/expert_sel_up_gate_silu.py:714-737)
+ *   tl_expert_select_up_gate_silu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
+ *   tl_expert_down_allreduce       expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
+ *                          (these two: the reference's own tensor-parallel layout, shared expert)
+ *   tl_rmsnorm_up_gate_silu  rmsnorm_up_gate_silu_op  .../ops/rmsnorm_up_gate_silu.py:26-44
+ *   tl_down_allreduce        down_allreduce_op        .../ops/down_allreduce.py:24-59
  *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
  *   tl_indexer_fp8_scores  sparse_index_op                .../ops/sparse_index.py:11-69
  *   tl_indexer_fp8_scores_paged  the same over KI pages    pd_vllm/profiles/mla_nsa.py:211-228
@@ -176,6 +184,64 @@ int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, const float* 
                         const int32_t* topk_idx, const float* topk_w, int64_t M, int64_t topk,
                         int64_t expert_begin, int64_t n_local, int64_t D, int64_t I,
                         void* y_bf16, void* stream);
+
+/* ---- The reference's MoE and dense-MLP operators in their own layout: one device's share of
+ * the tensor-parallel split of every expert's intermediate dim (I rows per expert).  Local
+ * expert 0 is the shared expert, 1 + j routed expert j.  Weights: tl_moe_pack_weight of the
+ * stacked [n_local * 2I, D] gate/up (per expert I gate rows, then I up rows) and
+ * [n_local * D, I] down matrices; fp32 block scales [n_local, 2I/128, D/128] and
+ * [n_local, D/128, I/128].  bf16 activations times bf16(fp32(q) * scale) weights, fp32
+ * accumulation (the goldens' bf16 reference weights).  At most 64 (token, position) pairs,
+ * x [M, D] within 64 KB (M <= 4 at D = 7168). */
+
+/* Routing of expert_select_up_gate_silu_op (golden _ref_expert_select_ds,
+ * glm_5/_dsa_v32/ops/expert_sel_up_gate_silu.py:714-737; n_groups = 1 is
+ * _ref_expert_select_glm5, deepseek_v3_2/ops/expert_sel_up_gate_silu.py:641-652):
+ * scores fp32 [M, n_routed] router logits, bias fp32 [n_routed] (nullable): s = sigmoid,
+ * choice on s + bias, limited to the topk_groups best of n_groups groups (score: the sum of
+ * a group's two largest biased scores; its largest without bias), top-k in descending
+ * order (lowest id first on ties); probs_out [M, topk] = the chosen s / their sum *
+ * route_scale, idx_out int32 [M, topk].  n_routed <= 256. */
+int tl_moe_route(const float* scores, const float* bias, int64_t M, int64_t n_routed, int64_t topk,
+                 int64_t n_groups, int64_t topk_groups, float route_scale, float* probs_out,
+                 int32_t* idx_out, void* stream);
+
+/* expert_select_up_gate_silu_op (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:23-48; golden
+ * :654-692): tl_moe_route, then for every token t and position p (0 = shared expert,
+ * 1 + j = its j-th selected expert) h[t, p, :] = bf16(silu(x_t . G^T) * (x_t . U^T)).
+ * x bf16 [M, D]; h bf16 [M, 1 + topk, I]; probs_out / idx_out as tl_moe_route.  Two
+ * launches (routing, gate/up); only the hit experts' weights are read. */
+int tl_expert_select_up_gate_silu(const void* x_bf16, const float* scores, const float* bias,
+                                  const void* w13_packed, const float* s13, int64_t M, int64_t n_routed,
+                                  int64_t topk, int64_t n_groups, int64_t topk_groups, float route_scale,
+                                  int64_t D, int64_t I, void* h_bf16, float* probs_out, int32_t* idx_out,
+                                  void* stream);
+
+/* expert_down_allreduce_op (deepseek_v3_2/ops/expert_down_allreduce.py:23-63; golden
+ * :445-468) at one device: h bf16 [M, 1 + topk, I] (tl_expert_select_up_gate_silu's), idx
+ * int32 / probs fp32 [M, topk] (distinct ids per token; ids outside [0, n_routed) are
+ * skipped): y[t] = bf16( sum_p bf16(w[t,p] * (h[t,p] . D_{e(t,p)}^T)) ), w = 1 for the
+ * shared position, fp32 sum; when x_in bf16 [M, D] is given, y = bf16(y + x_in) (the
+ * allreduce epilogue's residual; across devices the partials would be summed first).
+ * y bf16 [M, D]. */
+int tl_expert_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const int32_t* idx,
+                             const float* probs, const void* x_in_bf16, int64_t M, int64_t n_routed,
+                             int64_t topk, int64_t D, int64_t I, void* y_bf16, void* stream);
+
+/* rmsnorm_up_gate_silu_op (deepseek_v3_2/ops/rmsnorm_up_gate_silu.py:26-44; golden
+ * :318-347): the dense MLP's device share as n_chunks chunks of I rows (chunk i = the
+ * reference's pseudo-expert i).  xn = bf16(x * 1/sqrt(mean(x^2) + eps) * gamma) in fp32,
+ * then h[t, i, :] = bf16(silu(xn_t . G_i^T) * (xn_t . U_i^T)).  x bf16 [M, D], gamma fp32
+ * [D] (16-byte aligned), h bf16 [M, n_chunks, I].  One launch. */
+int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, float eps, const void* w13_packed,
+                            const float* s13, int64_t M, int64_t n_chunks, int64_t D, int64_t I, void* h_bf16,
+                            void* stream);
+
+/* down_allreduce_op (deepseek_v3_2/ops/down_allreduce.py:24-59; golden :293-320):
+ * y[t] = bf16( sum_i bf16(h[t,i] . D_i^T) ) (+ x_in as tl_expert_down_allreduce).
+ * h bf16 [M, n_chunks, I], y bf16 [M, D]. */
+int tl_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const void* x_in_bf16,
+                      int64_t M, int64_t n_chunks, int64_t D, int64_t I, void* y_bf16, void* stream);
 
 /* RMSNorm with optional activation quantisation (rmsnorm_quant_op / rmsnorm_op,
  * ops/rmsnorm_quant.py:19-63; norm of tilert/models/common.py:92-133 without residual).

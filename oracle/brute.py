@@ -63,3 +63,29 @@ def topk_fp64(scores, valid, k):
             out[i, j] = best
             taken[best] = True
     return out
+
+
+def expert_select_py(logits, bias, topk, n_groups, topk_groups, route_scale):
+    """Routing by plain Python sorting, one token at a time (fp64 sigmoid): per group the
+    sum of its two largest biased scores (its max without bias), keep the topk_groups best
+    groups, then the topk best biased scores among their experts (descending), weights =
+    unbiased sigmoid / their sum * route_scale."""
+    import math
+    T, n = len(logits), len(logits[0])
+    gsz = n // n_groups
+    W, I = [], []
+    for t in range(T):
+        s = [1.0 / (1.0 + math.exp(-float(v))) for v in logits[t]]
+        b = [s[e] + (float(bias[e]) if bias is not None else 0.0) for e in range(n)]
+        groups = list(range(n_groups))
+        if n_groups > 1:
+            def gscore(g):
+                vals = sorted(b[g * gsz:(g + 1) * gsz], reverse=True)
+                return vals[0] if bias is None else vals[0] + vals[1]
+            groups = sorted(groups, key=lambda g: -gscore(g))[:topk_groups]
+        allowed = [e for g in groups for e in range(g * gsz, (g + 1) * gsz)]
+        chosen = sorted(allowed, key=lambda e: -b[e])[:topk]
+        tot = sum(s[e] for e in chosen)
+        I.append(chosen)
+        W.append([s[e] / tot * route_scale for e in chosen])
+    return W, I

@@ -387,3 +387,136 @@ def rmsnorm_projq_wqb(q: torch.Tensor, q_norm_weight: torch.Tensor, wq_b: torch.
     w = weight_dequant(wq_b, wq_b_s).to(torch.bfloat16)
     out = torch.matmul(qr, w.T).view(*q.shape[:-1], n_heads, nope_dim + rope_dim)
     return out[..., :nope_dim], out[..., nope_dim:]
+
+
+# ------------------------------------------------ reference-layout MoE and dense MLP ops
+def expert_select(scores: torch.Tensor, bias: torch.Tensor | None, topk: int, n_groups: int,
+                  topk_groups: int, route_scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Routing of ``expert_select_up_gate_silu`` for logits [T, n_routed] (fp32):
+    ``_ref_expert_select_ds`` (glm_5/_dsa_v32/ops/expert_sel_up_gate_silu.py:714-737; DeepSeek
+    V3.2 uses 8 groups, top-4 groups) and ``_ref_expert_select_glm5`` (deepseek_v3_2/ops/
+    expert_sel_up_gate_silu.py:641-652, = one group).  sigmoid, + bias for the choice only,
+    group-limited (group score = sum of the group's top-2 biased scores, or its max without
+    bias), top-k in descending order, weights = the chosen UNBIASED sigmoid scores
+    normalised to sum 1, times route_scale.  Returns (weights fp32 [T, topk], indices int64
+    [T, topk])."""
+    s = scores.float().sigmoid()
+    orig = s
+    if bias is not None:
+        s = s + bias.float()
+    T, n = s.shape
+    if n_groups > 1:
+        g = s.view(T, n_groups, -1)
+        gs = g.amax(dim=-1) if bias is None else g.topk(2, dim=-1)[0].sum(dim=-1)
+        keep = gs.topk(topk_groups, dim=-1)[1]
+        mask = s.new_ones(T, n_groups, dtype=torch.bool).scatter_(1, keep, False)
+        s = g.masked_fill(mask.unsqueeze(-1), float("-inf")).flatten(1)
+    idx = torch.topk(s, topk, dim=-1)[1]
+    w = orig.gather(-1, idx)
+    w = w / w.sum(dim=-1, keepdim=True)
+    w = w * route_scale
+    return w, idx
+
+
+def expert_select_up_gate_silu(x: torch.Tensor, idx: torch.Tensor, gq: torch.Tensor, gs: torch.Tensor,
+                               uq: torch.Tensor, us: torch.Tensor) -> torch.Tensor:
+    """``ExpertSelectUpGateSiLU.golden_forward`` (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:
+    654-692) at one device's share: x bf16 [T, D]; idx [T, topk] routed ids; gq/uq e4m3fn
+    [1 + n_routed, I, D] with block scales (expert 0 = the shared expert, routed expert j at
+    1 + j), dequantised then rounded to bf16 (:545-552).  Per token: the shared expert, then
+    the selected experts in idx order: h = bf16(silu(x G^T) * (x U^T)) in fp32 ->
+    [T, 1 + topk, I] bf16."""
+    T = x.shape[0]
+    xf = x.float()
+    cache: dict[int, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    def w(e):
+        if e not in cache:
+            cache[e] = (weight_dequant(gq[e], gs[e]).to(torch.bfloat16).float(),
+                        weight_dequant(uq[e], us[e]).to(torch.bfloat16).float())
+        return cache[e]
+    out = []
+    for t in range(T):
+        rows = []
+        for e in [0] + [1 + int(j) for j in idx[t]]:
+            g, u = w(e)
+            rows.append(swiglu(xf[t] @ g.T, xf[t] @ u.T))
+        out.append(torch.stack(rows))
+    return torch.stack(out).to(torch.bfloat16)
+
+
+def expert_down_allreduce(h: torch.Tensor, idx: torch.Tensor, probs: torch.Tensor, dq: torch.Tensor,
+                          ds: torch.Tensor, x_in: torch.Tensor | None = None) -> torch.Tensor:
+    """``ExpertDownAllReduce.golden_forward`` (deepseek_v3_2/ops/expert_down_allreduce.py:
+    445-468) at one device's share: h bf16 [T, 1 + topk, I]; dq e4m3fn [1 + n_routed, D, I]
+    + block scales, dequantised then rounded to bf16 (:389-393).  Per token the shared term
+    h[t,0] D_0^T and the routed terms probs[t,j] * (h[t,1+j] D_{1+idx}^T), each rounded to
+    bf16, summed in fp32 and rounded once -> [T, D] bf16.  ``x_in`` (the residual the op's
+    allreduce epilogue adds; single-GPU golden of padded_allreduce_add.py:100-114 is
+    x_in + allreduce(partial)) is added to the bf16 sum when given."""
+    T = h.shape[0]
+    cache: dict[int, torch.Tensor] = {}
+
+    def w(e):
+        if e not in cache:
+            cache[e] = weight_dequant(dq[e], ds[e]).to(torch.bfloat16).float()
+        return cache[e]
+    out = []
+    for t in range(T):
+        acc = (h[t, 0].float() @ w(0).T).to(torch.bfloat16).float()
+        for j in range(idx.shape[1]):
+            term = (h[t, 1 + j].float() @ w(1 + int(idx[t, j])).T) * probs[t, j].float()
+            acc = acc + term.to(torch.bfloat16).float()
+        out.append(acc)
+    y = torch.stack(out).to(torch.bfloat16)
+    if x_in is not None:
+        y = (y.float() + x_in.float()).to(torch.bfloat16)
+    return y
+
+
+def rms_norm_f32(x: torch.Tensor, gamma: torch.Tensor, eps: float) -> torch.Tensor:
+    """``torch.nn.functional.rms_norm(x.float(), [dim], gamma, eps)`` as the dense-MLP golden
+    calls it (rmsnorm_up_gate_silu.py:333-335), fp32 out."""
+    xf = x.float()
+    return xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * gamma.float()
+
+
+def rmsnorm_up_gate_silu(x: torch.Tensor, gamma: torch.Tensor, eps: float, gq: torch.Tensor, gs: torch.Tensor,
+                         uq: torch.Tensor, us: torch.Tensor, bf16_operands: bool) -> torch.Tensor:
+    """``RMSNormUpGateSiLU.golden_forward`` (deepseek_v3_2/ops/rmsnorm_up_gate_silu.py:323-347):
+    x bf16 [T, D] -> fp32 RMSNorm -> for each of the device's chunks i (gq/uq e4m3fn
+    [n_chunks, I, D] + block scales): h[t,i] = bf16(silu(xn G_i^T) * (xn U_i^T)) ->
+    [T, n_chunks, I] bf16.  ``bf16_operands=False`` is the golden (fp32 normalised x, fp32
+    dequantised weights); ``True`` rounds both operands to bf16 first, the numerics of the
+    reference's FP16MMA/BF16MMA kernels (modules/mlp.py:24-29 selects FP16MMA) that the HIP
+    kernel follows."""
+    xn = rms_norm_f32(x, gamma, eps)
+    if bf16_operands:
+        xn = xn.to(torch.bfloat16).float()
+    out = []
+    for i in range(gq.shape[0]):
+        g = weight_dequant(gq[i], gs[i])
+        u = weight_dequant(uq[i], us[i])
+        if bf16_operands:
+            g, u = g.to(torch.bfloat16).float(), u.to(torch.bfloat16).float()
+        out.append(swiglu(xn @ g.T, xn @ u.T))
+    return torch.stack(out, dim=1).to(torch.bfloat16)
+
+
+def down_allreduce(h: torch.Tensor, dq: torch.Tensor, ds: torch.Tensor, bf16_weights: bool,
+                   x_in: torch.Tensor | None = None) -> torch.Tensor:
+    """``DownAllReduce.golden_forward`` (deepseek_v3_2/ops/down_allreduce.py:293-320): h bf16
+    [T, n_chunks, I], dq e4m3fn [n_chunks, D, I] + block scales; per token the chunk terms
+    h[t,i] D_i^T, each rounded to bf16, summed in fp32, rounded once -> [T, D] bf16 (+ x_in
+    as in ``expert_down_allreduce``).  ``bf16_weights`` rounds the dequantised weights to bf16
+    (the kernel's numerics); the golden keeps them fp32."""
+    terms = []
+    for i in range(dq.shape[0]):
+        w = weight_dequant(dq[i], ds[i])
+        if bf16_weights:
+            w = w.to(torch.bfloat16).float()
+        terms.append((h[:, i].float() @ w.T).to(torch.bfloat16).float())
+    y = torch.stack(terms).sum(0).to(torch.bfloat16)
+    if x_in is not None:
+        y = (y.float() + x_in.float()).to(torch.bfloat16)
+    return y

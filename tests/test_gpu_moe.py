@@ -31,8 +31,8 @@ def _run(M, E, D, I, topk, n_experts, e0, seed, idx=None, w=None):
         idx, w = synth.routing(M, n_experts, topk, g)
     ex = moe.LocalExperts(*(t.to(cuda) for t in (W["gate"][0], W["gate"][1], W["up"][0], W["up"][1],
                                                    W["down"][0], W["down"][1])), expert_begin=e0)
-    h = moe.expert_select_up_gate_silu(x.to(cuda), idx.to(cuda), ex)
-    y = moe.expert_down_allreduce(h, ex, idx.to(cuda), w.to(cuda))
+    h = moe.ep_gate_up_swiglu(x.to(cuda), idx.to(cuda), ex)
+    y = moe.ep_down_combine(h, ex, idx.to(cuda), w.to(cuda))
     rh, hits = ref.moe_gate_up(x, W["gate"][0], W["gate"][1], W["up"][0], W["up"][1], idx, e0)
     ry = ref.moe_down(rh, hits, W["down"][0], W["down"][1], idx, w, e0)
     torch.cuda.synchronize()

@@ -38,13 +38,13 @@ def test_moe_rejects_host_outputs(cuda):
     idx = torch.zeros(1, 2, dtype=torch.int32, device=cuda)
     w = torch.ones(1, 2, device=cuda)
     with pytest.raises(ValueError):
-        moe.expert_select_up_gate_silu(x, idx, ex, torch.empty(2, 1, 128, dtype=torch.bfloat16))
-    h = moe.expert_select_up_gate_silu(x, idx, ex)
+        moe.ep_gate_up_swiglu(x, idx, ex, torch.empty(2, 1, 128, dtype=torch.bfloat16))
+    h = moe.ep_gate_up_swiglu(x, idx, ex)
     with pytest.raises(ValueError):
-        moe.expert_down_allreduce(h, ex, idx, w, vec_out=torch.empty(1, 256, dtype=torch.bfloat16))
+        moe.ep_down_combine(h, ex, idx, w, vec_out=torch.empty(1, 256, dtype=torch.bfloat16))
     ex.w2 = ex.w2.cpu()
     with pytest.raises(ValueError):
-        moe.expert_down_allreduce(h, ex, idx, w)
+        moe.ep_down_combine(h, ex, idx, w)
 
 
 def test_fp8_gemm_rejects_host_output(cuda):

@@ -380,3 +380,104 @@ def test_rmsnorm_projq_wqb_vs_fp64_and_head_split():
     q1, s1 = ref.weight_quant(wq1)
     n1, _ = ref.rmsnorm_projq_wqb(q, gamma, q1, s1, heads)
     assert torch.equal(n1[:, 0, 5].float(), (qr[:, 17].float() * wd.new_tensor(1.0).float()).to(torch.bfloat16).float())
+
+
+# ------------------------------------------------------------- routing (expert select)
+@pytest.mark.parametrize("n_groups,topk_groups,with_bias", [(8, 4, True), (8, 4, False), (1, 1, True)])
+def test_expert_select_vs_python_sort(n_groups, topk_groups, with_bias):
+    g = synth.gen(40 + n_groups)
+    logits = torch.randn(6, 256, generator=g)
+    bias = torch.randn(256, generator=g) * 0.1 if with_bias else None
+    w, idx = ref.expert_select(logits, bias, 8, n_groups, topk_groups, 2.5)
+    bw, bi = brute.expert_select_py(logits.tolist(), bias.tolist() if bias is not None else None, 8, n_groups,
+                                    topk_groups, 2.5)
+    assert idx.tolist() == bi
+    assert torch.allclose(w.double(), torch.tensor(bw, dtype=torch.float64), rtol=1e-6, atol=0)
+
+
+def test_expert_select_invariants():
+    g = synth.gen(44)
+    logits = torch.randn(16, 256, generator=g) * 3
+    bias = torch.randn(256, generator=g)
+    w, idx = ref.expert_select(logits, bias, 8, 8, 4, 2.5)
+    assert torch.allclose(w.sum(-1), torch.full((16,), 2.5), rtol=1e-6)
+    for t in range(16):
+        assert len(set(idx[t].tolist())) == 8
+        assert len({int(e) // 32 for e in idx[t]}) <= 4  # group-limited to 4 of 8 groups
+        b = logits[t].sigmoid() + bias
+        assert torch.all(b[idx[t]][:-1] >= b[idx[t]][1:])  # descending by biased score
+        # the bias steers the choice only: weights are the unbiased sigmoid scores
+        sel = logits[t].sigmoid()[idx[t]]
+        assert torch.allclose(w[t], sel / sel.sum() * 2.5, rtol=1e-6)
+
+
+def test_expert_select_bias_changes_choice_not_weights():
+    logits = torch.zeros(1, 256)
+    logits[0, :8] = 1.0  # the unbiased top-8
+    bias = torch.zeros(256)
+    bias[100:108] = 5.0  # a large bias moves the choice to 100..107 (one group-pair)
+    w, idx = ref.expert_select(logits, bias, 8, 8, 4, 2.5)
+    assert sorted(idx[0].tolist()) == list(range(100, 108))
+    assert torch.allclose(w, torch.full((1, 8), 2.5 / 8))
+
+
+# ----------------------------------------------------------- reference-layout MoE goldens
+def _tp_experts(E, D, I, g):
+    out = {}
+    for name, (n, k) in (("gate", (I, D)), ("up", (I, D)), ("down", (D, I))):
+        q, s = zip(*[ref.weight_quant(synth.weight_fp32(n, k, g)) for _ in range(E)])
+        out[name] = (torch.stack(q), torch.stack(s))
+    return out
+
+
+def test_expert_select_up_gate_silu_and_down_vs_fp64():
+    """The per-position goldens against fp64 recomputation with explicit loops over
+    (token, position): the shared expert at position 0, routed expert j at 1 + idx."""
+    g = synth.gen(45)
+    E, D, I, T, k = 6, 256, 128, 2, 3
+    W = _tp_experts(E, D, I, g)
+    x = synth.activations(T, D, g)
+    idx = torch.tensor([[4, 0, 2], [1, 4, 3]])
+    probs = torch.tensor([[0.5, 0.3, 0.2], [0.1, 0.6, 0.3]])
+    h = ref.expert_select_up_gate_silu(x, idx, *W["gate"], *W["up"])
+    assert h.shape == (T, 1 + k, I)
+    xd = x.double()
+    for t in range(T):
+        for p, e in enumerate([0] + [1 + int(j) for j in idx[t]]):
+            gw = ref.weight_dequant(*[a[e] for a in W["gate"]]).to(torch.bfloat16).double()
+            uw = ref.weight_dequant(*[a[e] for a in W["up"]]).to(torch.bfloat16).double()
+            a, b = xd[t] @ gw.T, xd[t] @ uw.T
+            want = (a / (1 + torch.exp(-a)) * b)
+            assert torch.allclose(h[t, p].double(), want, rtol=1e-2, atol=1e-3)
+    xin = synth.activations(T, D, g)
+    y = ref.expert_down_allreduce(h, idx, probs, *W["down"], x_in=xin)
+    for t in range(T):
+        acc = torch.zeros(D, dtype=torch.float64)
+        for p, e in enumerate([0] + [1 + int(j) for j in idx[t]]):
+            dw = ref.weight_dequant(*[a[e] for a in W["down"]]).to(torch.bfloat16).double()
+            wt = 1.0 if p == 0 else float(probs[t, p - 1])
+            acc += wt * (h[t, p].double() @ dw.T)
+        assert torch.allclose(y[t].double(), acc + xin[t].double(), rtol=2e-2, atol=2e-2)
+
+
+def test_dense_mlp_goldens_vs_fp64_and_variants():
+    g = synth.gen(46)
+    C, D, I, T = 3, 256, 128, 2
+    W = _tp_experts(C, D, I, g)
+    x = synth.activations(T, D, g)
+    gamma = torch.rand(D, generator=g) + 0.5
+    h32 = ref.rmsnorm_up_gate_silu(x, gamma, 1e-6, *W["gate"], *W["up"], bf16_operands=False)
+    h16 = ref.rmsnorm_up_gate_silu(x, gamma, 1e-6, *W["gate"], *W["up"], bf16_operands=True)
+    xd = x.double()
+    xn = xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + 1e-6) * gamma.double()
+    for i in range(C):
+        a = xn @ ref.weight_dequant(*[w[i] for w in W["gate"]]).double().T
+        b = xn @ ref.weight_dequant(*[w[i] for w in W["up"]]).double().T
+        want = a / (1 + torch.exp(-a)) * b
+        assert torch.allclose(h32[:, i].double(), want, rtol=1e-2, atol=1e-4)
+    # rounding the operands to bf16 moves the result by about a bf16 step, no more
+    rel = (torch.norm(h16.float() - h32.float()) / torch.norm(h32.float())).item()
+    assert 0 < rel < 1e-2
+    y = ref.down_allreduce(h16, *W["down"], bf16_weights=False)
+    acc = sum(h16[:, i].double() @ ref.weight_dequant(*[w[i] for w in W["down"]]).double().T for i in range(C))
+    assert torch.allclose(y.double(), acc, rtol=2e-2, atol=2e-2)

@@ -42,6 +42,17 @@ SIGNATURES: dict[str, tuple] = {
                                      _i64, _i64, _i64, _i64, _c_void_p, _c_void_p]),
     "tl_moe_down_combine": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "tl_moe_route": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _c_void_p,
+                            _c_void_p, _c_void_p]),
+    "tl_expert_select_up_gate_silu": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                             _i64, _i64, ctypes.c_float, _i64, _i64, _c_void_p, _c_void_p,
+                                             _c_void_p, _c_void_p]),
+    "tl_expert_down_allreduce": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                        _i64, _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "tl_rmsnorm_up_gate_silu": (_int, [_c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _c_void_p, _i64, _i64,
+                                       _i64, _i64, _c_void_p, _c_void_p]),
+    "tl_down_allreduce": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _c_void_p,
+                                 _c_void_p]),
     "tl_rmsnorm_quant": (_int, [_c_void_p, _c_void_p, ctypes.c_float, _i64, _i64, _c_void_p, _c_void_p,
                                 _c_void_p, _int, _c_void_p]),
     "tl_indexer_fp8_scores": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _c_void_p,

@@ -1,0 +1,578 @@
+// The reference's MoE and dense-MLP operators in their own tensor layout: one device's share
+// of the tensor-parallel split of every expert's intermediate dim (I = moe_inter_dim / 8 =
+// 256 rows of gate, up and down per expert and device).
+//
+//  * expert_select_up_gate_silu_op (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:23-48):
+//    routing on the device -- sigmoid, + e_score_correction_bias for the choice only,
+//    group-limited top-k, the chosen unbiased scores normalised and scaled by route_scale
+//    (golden _ref_expert_select_ds, glm_5/_dsa_v32/ops/expert_sel_up_gate_silu.py:714-737;
+//    one group = _ref_expert_select_glm5) -- then gate/up + SwiGLU of the shared expert and
+//    the token's selected experts into hidden_out [T, 1 + topk, I] (golden :654-692).
+//  * expert_down_allreduce_op (.../expert_down_allreduce.py:23-63, golden :445-468):
+//    y[t] = bf16( sum over positions p of bf16(w[t,p] * (h[t,p] . D_{e(t,p)}^T)) ), the
+//    shared position weighing 1, plus the residual x_in when given (the single-GPU form of
+//    the allreduce epilogue, padded_allreduce_add.py:100-114).
+//  * rmsnorm_up_gate_silu_op / down_allreduce_op (.../rmsnorm_up_gate_silu.py:26-44, golden
+//    :318-347; .../down_allreduce.py:24-59, golden :293-320): the dense MLP's device share as
+//    n_chunks pseudo-experts of I rows that every token uses, the RMSNorm fused into the
+//    gate/up kernel.
+//
+// Local expert numbering: 0 = the shared expert, 1 + j = routed expert j (the reference's
+// stacking, expert_sel_up_gate_silu.py:478-499); for the dense MLP, chunk i.  Weights use
+// the MoE kernels' tile-major fragment packing (tl_moe_pack_weight) of the stacked
+// [n_local * 2I, D] gate/up and [n_local * D, I] down matrices.
+//
+// Numerics: bf16 activations times fp8 weights dequantised in registers to
+// bf16(fp32(q) * scale), v_mfma_f32_16x16x32_bf16, fp32 accumulation -- the goldens' own
+// bf16 weights (expert_sel_up_gate_silu.py:545-552, expert_down_allreduce.py:389-393).
+//
+// Each token's (position -> local expert, weight) pairs are held one per lane (pair p =
+// token p / P, position p % P; M * P <= 64), so hit sets, output positions and routing
+// weights are lane shuffles, with no host synchronisation and no dependent loads.
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+#include "moe_common.h"
+#include "../../include/tilert_amd.h"
+
+namespace tl {
+
+constexpr int kRefWaves = 8;
+constexpr int kRefMaskWords = 5;            // local experts < 320 (shared + 256 routed)
+constexpr int kRefMaxLocal = 64 * kRefMaskWords;
+constexpr int kRefMaxRouted = 256;          // 4 per lane in the routing wave
+constexpr int kRefLdsX = 64 * 1024;         // staged activations (x or gathered h)
+constexpr int kRefDepth = 2;                // weight blocks in flight per wave
+
+// Hit set over local experts, wave-uniform (scalar registers).
+struct ExpertMask {
+  uint64_t w[kRefMaskWords];
+  int n;
+};
+
+__device__ inline uint64_t wave_or64(uint64_t m) {
+  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo |= __shfl_xor(lo, o);
+    hi |= __shfl_xor(hi, o);
+  }
+  lo = __builtin_amdgcn_readfirstlane(lo);
+  hi = __builtin_amdgcn_readfirstlane(hi);
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
+// The set of local experts the lanes name (e < 0: none).
+__device__ inline ExpertMask lanes_mask(int e) {
+  ExpertMask m;
+  m.n = 0;
+#pragma unroll
+  for (int k = 0; k < kRefMaskWords; ++k) {
+    const uint64_t b = (e >= 64 * k && e < 64 * k + 64) ? (1ull << (e - 64 * k)) : 0ull;
+    m.w[k] = wave_or64(b);
+    m.n += __builtin_popcountll(m.w[k]);
+  }
+  return m;
+}
+
+// The n-th hit local expert in ascending order.
+__device__ inline int mask_nth(const ExpertMask& m, int n) {
+#pragma unroll
+  for (int k = 0; k < kRefMaskWords; ++k) {
+    const int c = __builtin_popcountll(m.w[k]);
+    if (n < c) return 64 * k + nth_set_bit(m.w[k], n);
+    n -= c;
+  }
+  return 0;
+}
+
+// This lane's pair: local expert (-1 past the M * P pairs, and for a routed id outside
+// [0, n_local - 1), which is ignored) and weight.  The loads are unconditional (clamped),
+// so wait counts of later loads stay exact.
+template <bool DENSE>
+__device__ inline void pair_lane(const int32_t* __restrict__ idx, const float* __restrict__ probs, int M, int P,
+                                 int topk, int n_local, int& e, float& w) {
+  const int lane = threadIdx.x & 63;
+  const int t = lane / P, pos = lane - t * P;
+  const bool live = lane < M * P;
+  if (DENSE) {
+    e = live ? pos : -1;
+    w = 1.f;
+    return;
+  }
+  const int q = min(t * topk + max(pos - 1, 0), M * topk - 1);
+  const int ie = idx[q];
+  const float pw = probs ? probs[q] : 0.f;
+  e = !live ? -1 : (pos == 0 ? 0 : (ie >= 0 && ie < n_local - 1 ? 1 + ie : -1));
+  w = pos == 0 ? 1.f : pw;
+}
+
+// Position of local expert e for token r (-1: the token does not use it) and its weight.
+// Every lane takes part in the shuffles.
+__device__ inline int token_pos(int pe, float pw, int P, int r, int e, float& w) {
+  int pos = -1;
+  w = 0.f;
+  for (int p = 0; p < P; ++p) {
+    const int ee = __shfl(pe, r * P + p);
+    const float ww = __shfl(pw, r * P + p);
+    if (ee == e && pos < 0) {
+      pos = p;
+      w = ww;
+    }
+  }
+  return pos;
+}
+
+// ------------------------------------------------------------------------ routing
+// One wave per token: lane l holds routed experts l, l + 64, l + 128, l + 192.
+__device__ inline bool better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
+
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ scores, const float* __restrict__ bias,
+                                                       int n, int topk, int n_groups, int topk_groups, float route_scale,
+                                                       float* __restrict__ probs, int32_t* __restrict__ idx) {
+  __shared__ float bl[kRefMaxRouted];
+  __shared__ float gscore[64];
+  __shared__ int gkeep[64];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  float s[4], b[4];
+  bool live[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = lane + 64 * i;
+    live[i] = e < n;
+    const float x = scores[static_cast<size_t>(t) * n + min(e, n - 1)];
+    s[i] = 1.0f / (1.0f + expf(-x));  // sigmoid
+    b[i] = live[i] ? s[i] + (bias ? bias[min(e, n - 1)] : 0.f) : -INFINITY;
+  }
+  if (n_groups > 1) {  // keep the topk_groups best groups (score: top-2 sum with bias, else max)
+    const int gsz = n / n_groups;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (live[i]) bl[lane + 64 * i] = b[i];
+    __syncthreads();
+    if (lane < n_groups) {
+      float m1 = -INFINITY, m2 = -INFINITY;
+      for (int j = 0; j < gsz; ++j) {
+        const float v = bl[lane * gsz + j];
+        if (v > m1) {
+          m2 = m1;
+          m1 = v;
+        } else if (v > m2) {
+          m2 = v;
+        }
+      }
+      gscore[lane] = bias ? m1 + m2 : m1;
+    }
+    __syncthreads();
+    if (lane < n_groups) {
+      int rank = 0;
+      for (int g = 0; g < n_groups; ++g) rank += better(gscore[g], g, gscore[lane], lane) ? 1 : 0;
+      gkeep[lane] = rank < topk_groups;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (live[i] && !gkeep[(lane + 64 * i) / gsz]) b[i] = -INFINITY;
+  }
+  // top-k by repeated wave arg-max (descending, lowest expert first on ties)
+  bool taken[4] = {false, false, false, false};
+  int my_e = 0;
+  float my_s = 0.f, sum = 0.f;
+  for (int r = 0; r < topk; ++r) {
+    float bv = -INFINITY;
+    int be = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (live[i] && !taken[i] && better(b[i], lane + 64 * i, bv, be)) {
+        bv = b[i];
+        be = lane + 64 * i;
+      }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oe = __shfl_xor(be, o);
+      if (better(ov, oe, bv, be)) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    const int owner = be & 63, slot = be >> 6;
+    float sv = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i == slot) sv = s[i];
+      if (lane == owner && i == slot) taken[i] = true;
+    }
+    sv = __shfl(sv, owner);
+    if (lane == r) {
+      my_e = be;
+      my_s = sv;
+    }
+    sum += sv;
+  }
+  if (lane < topk) {
+    idx[t * topk + lane] = my_e;
+    probs[t * topk + lane] = my_s / sum * route_scale;
+  }
+}
+
+// ------------------------------------------------------------------------ gate/up
+// Work item = (hit local expert, 16-row tile); a persistent grid strides over the items.
+// x [M, D] bf16 is staged in LDS once per workgroup (DENSE: RMS-normalised there, in fp32,
+// rounded to bf16); the waves stream weight fragments kRefDepth blocks ahead and read their
+// activation operands from LDS.  The epilogue writes token r's row to every position p at
+// which r uses the expert: h [M, P, I].
+template <bool DENSE>
+__global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ w13,
+    const float* __restrict__ s13, const int32_t* __restrict__ idx, int M, int P, int topk, int n_local, int D, int I,
+    uint16_t* __restrict__ h) {
+  extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
+  __shared__ float red[kRefWaves - 1][2][4][64];
+  __shared__ float ssq[16][kRefWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int pe;
+  float pw;
+  pair_lane<DENSE>(idx, nullptr, M, P, topk, n_local, pe, pw);
+  const int x16 = M * D / 8;
+  stage_commit(xl, stage_issue(x, x16), x16);
+  const ExpertMask mask = lanes_mask(pe);
+  __syncthreads();
+  if (DENSE) {  // RMSNorm of the staged rows: x * (1 / sqrt(mean(x^2) + eps)) * gamma, fp32
+    const int c16 = D / 8;
+    for (int m = 0; m < M; ++m) {
+      float acc = 0.f;
+      for (int c = threadIdx.x; c < c16; c += blockDim.x) {
+        const u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = bf16_to_f32(v[j] & 0xffffu), hi = bf16_to_f32(v[j] >> 16);
+          acc += lo * lo + hi * hi;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+      if (lane == 0) ssq[m][wave] = acc;
+    }
+    __syncthreads();
+    for (int m = 0; m < M; ++m) {
+      float ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < kRefWaves; ++w) ss += ssq[m][w];
+      const float rs = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+      for (int c = threadIdx.x; c < c16; c += blockDim.x) {
+        u32x4 v = reinterpret_cast<u32x4*>(xl + m * D)[c];
+        const v4f g0 = *reinterpret_cast<const v4f*>(gamma + 8 * c);
+        const v4f g1 = *reinterpret_cast<const v4f*>(gamma + 8 * c + 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float ga = j < 2 ? g0[2 * j] : g1[2 * j - 4], gb = j < 2 ? g0[2 * j + 1] : g1[2 * j - 3];
+          v[j] = f32_to_bf16(bf16_to_f32(v[j] & 0xffffu) * rs * ga) |
+                 (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(v[j] >> 16) * rs * gb)) << 16);
+        }
+        reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
+      }
+    }
+    __syncthreads();
+  }
+  const int KB = D >> 7, tiles = I >> 4, rows_e = 2 * I;
+  const int r = lane & 15, g = lane >> 4;
+  const uint16_t* xrow = xl + min(r, M - 1) * D;
+  const int n = wave < KB ? (KB - wave + kRefWaves - 1) / kRefWaves : 0;  // K blocks wave + i * 8
+
+  for (int item = blockIdx.x; item < mask.n * tiles; item += gridDim.x) {
+    const int slot = item / tiles, rt = item - slot * tiles;
+    const int e = mask_nth(mask, slot);
+    const uint8_t* gate = w13 + (static_cast<size_t>(e) * (rows_e >> 4) + rt) * KB * 2048;
+    const uint8_t* up = gate + static_cast<size_t>(tiles) * KB * 2048;
+    const float* gs = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((rt * 16) >> 7)) * KB;
+    const float* us = s13 + (static_cast<size_t>(e) * (rows_e >> 7) + ((I + rt * 16) >> 7)) * KB;
+    v4f ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    struct Ops {
+      v8i wg, wu;
+      float gs, us;
+    };
+    Ops buf[kRefDepth];
+    ring_pipeline(
+        n, buf,
+        [&](int i, Ops& o) {
+          const int kb = wave + i * kRefWaves;
+          o.wg = load_fragment(gate + static_cast<size_t>(kb) * 2048, lane);
+          o.wu = load_fragment(up + static_cast<size_t>(kb) * 2048, lane);
+          o.gs = load_f32_vector(gs + kb);
+          o.us = load_f32_vector(us + kb);
+        },
+        [&](int i, const Ops& o) {
+          const int kb = wave + i * kRefWaves;
+          const uint16_t* xk = xrow + kb * kBlock;
+          const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const v8bf xa = *reinterpret_cast<const v8bf*>(xk + off[j]);
+            ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wg[2 * j], o.wg[2 * j + 1], o.gs), xa, ag, 0, 0, 0);
+            au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wu[2 * j], o.wu[2 * j + 1], o.us), xa, au, 0, 0, 0);
+          }
+        });
+    if (wave > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        red[wave - 1][0][j][lane] = ag[j];
+        red[wave - 1][1][j][lane] = au[j];
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < kRefWaves - 1; ++w)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          ag[j] += red[w][0][j][lane];
+          au[j] += red[w][1][j][lane];
+        }
+      float unused;
+      const int pos = token_pos(pe, pw, P, min(r, M - 1), e, unused);
+      if (r < M && pos >= 0) {
+        uint16_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = f32_to_bf16(silu(ag[j]) * au[j]);
+        uint16_t* dst = h + (static_cast<size_t>(r) * P + pos) * I + rt * 16 + 4 * g;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                    o[2] | (static_cast<uint32_t>(o[3]) << 16));
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// -------------------------------------------------------------------- down + combine
+// One workgroup per 16-row output tile.  The rows each hit expert multiplies -- token r's
+// h row at the position where r uses it, zero where r does not -- are gathered into LDS as
+// [slot][M][I]; wave w takes slots w, w + 8, ... with all their K blocks (kRefDepth weight
+// blocks in flight), so each slot's product is complete in one wave, which then adds the
+// per-token terms bf16(weight * product) (the goldens' per-term rounding) to its fp32
+// partial.  The 8 wave partials are summed in wave order (deterministic), rounded to bf16,
+// and the residual x_in, when given, is added and rounded again.
+template <bool DENSE>
+__global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
+    const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
+    const int32_t* __restrict__ idx, const float* __restrict__ probs, const uint16_t* __restrict__ x_in, int M,
+    int P, int topk, int n_local, int D, int I, uint16_t* __restrict__ y) {
+  extern __shared__ __align__(16) uint16_t hl[];  // [n_hit][M][I]
+  __shared__ float red[kRefWaves][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int pe;
+  float pw;
+  pair_lane<DENSE>(idx, probs, M, P, topk, n_local, pe, pw);
+  const ExpertMask mask = lanes_mask(pe);
+  const int KB = I >> 7;
+  const int r = lane & 15, g = lane >> 4;
+  const int row = min(r, M - 1);
+  const int rt = blockIdx.x;
+  // gather: wave w fills slots w, w + 8, ... (16-byte chunks; rows a token does not use
+  // are zero)
+  const int c_row = I / 8;
+  for (int j = wave; j < mask.n; j += kRefWaves) {
+    const int e = mask_nth(mask, j);
+    for (int t = 0; t < M; ++t) {
+      float unused;
+      const int pos = token_pos(pe, pw, P, t, e, unused);
+      const u32x4* src = reinterpret_cast<const u32x4*>(h + (static_cast<size_t>(t) * P + max(pos, 0)) * I);
+      u32x4* dst = reinterpret_cast<u32x4*>(hl + (static_cast<size_t>(j) * M + t) * I);
+      for (int c = lane; c < c_row; c += 64) dst[c] = pos >= 0 ? src[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __syncthreads();
+  v4f yacc = {0.f, 0.f, 0.f, 0.f};
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+  const int my_slots = wave < mask.n ? (mask.n - wave + kRefWaves - 1) / kRefWaves : 0;
+  const int n = my_slots * KB;  // item i: slot wave + (i / KB) * 8, K block i % KB
+  struct Ops {
+    v8i w;
+    float sc;
+  };
+  Ops buf[kRefDepth];
+  ring_pipeline(
+      n, buf,
+      [&](int i, Ops& o) {
+        const int j = wave + (i / KB) * kRefWaves, kb = i % KB;
+        const int e = mask_nth(mask, j);
+        o.w = load_fragment(w2 + ((static_cast<size_t>(e) * (D >> 4) + rt) * KB + kb) * 2048, lane);
+        o.sc = load_f32_vector(s2 + (static_cast<size_t>(e) * (D >> 7) + ((rt * 16) >> 7)) * KB + kb);
+      },
+      [&](int i, const Ops& o) {
+        const int j = wave + (i / KB) * kRefWaves, kb = i % KB;
+        const ActOperand xa = lds_act(hl + (static_cast<size_t>(j) * M + row) * I + kb * kBlock, g);
+        acc = mfma_block_bf16(o.w, o.sc, xa, acc);
+        if (kb == KB - 1) {  // the slot's product is complete: add its weighted term
+          float wt;
+          token_pos(pe, pw, P, row, mask_nth(mask, j), wt);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            yacc[q] += bf16_to_f32(f32_to_bf16(acc[q] * wt));
+            acc[q] = 0.f;
+          }
+        }
+      });
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[wave][q][lane] = yacc[q];
+  __syncthreads();
+  if (wave == 0 && r < M) {
+    v4f s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kRefWaves; ++w)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] += red[w][q][lane];
+    uint16_t o[4];
+    const size_t off = static_cast<size_t>(r) * D + rt * 16 + 4 * g;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      o[q] = f32_to_bf16(s[q]);
+      if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(x_in[off + q]));
+    }
+    *reinterpret_cast<uint2*>(y + off) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                    o[2] | (static_cast<uint32_t>(o[3]) << 16));
+  }
+}
+
+static int check_common(const char* who, int64_t M, int64_t P, int64_t D, int64_t I) {
+  if (M < 1 || M * P > 64) { set_error("%s: M=%lld with %lld positions per token: at most 64 pairs", who, (long long)M, (long long)P); return kErrUnsupported; }
+  if (D <= 0 || I <= 0 || D % kBlock || I % kBlock) { set_error("%s: D=%lld and I=%lld must be positive multiples of 128", who, (long long)D, (long long)I); return kErrArg; }
+  if (D > (1 << 16) || I > (1 << 16)) { set_error("%s: D or I too large", who); return kErrArg; }
+  return kOk;
+}
+
+static int launch_gate_up(bool dense, const void* x, const float* gamma, float eps, const void* w13, const float* s13,
+                          const int32_t* idx, int64_t M, int64_t P, int64_t topk, int64_t n_local, int64_t D, int64_t I,
+                          void* h, hipStream_t st) {
+  const int64_t x_bytes = M * D * 2;
+  if (x_bytes > kRefLdsX) { set_error("gate/up: M * D * 2 = %lld bytes of activations exceed %d", (long long)x_bytes, kRefLdsX); return kErrUnsupported; }
+  const int64_t max_items = std::min<int64_t>(n_local, M * P) * (I / 16);
+  const int grid = static_cast<int>(std::min<int64_t>(max_items, 512));
+  const void* fn = dense ? reinterpret_cast<const void*>(ref_gate_up_kernel<true>) : reinterpret_cast<const void*>(ref_gate_up_kernel<false>);
+  if (int rc = allow_dynamic_lds(fn, kRefLdsX, "gate/up")) return rc;
+  if (dense)
+    hipLaunchKernelGGL(ref_gate_up_kernel<true>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(x_bytes), st,
+                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, idx, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
+                       (int)I, (uint16_t*)h);
+  else
+    hipLaunchKernelGGL(ref_gate_up_kernel<false>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(x_bytes), st,
+                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, idx, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
+                       (int)I, (uint16_t*)h);
+  return check_launch("gate/up");
+}
+
+static int launch_down(bool dense, const void* h, const void* w2, const float* s2, const int32_t* idx, const float* probs,
+                       const void* x_in, int64_t M, int64_t P, int64_t topk, int64_t n_local, int64_t D, int64_t I, void* y,
+                       hipStream_t st) {
+  const int64_t max_hit = std::min<int64_t>(n_local, M * P);
+  const int64_t lds = max_hit * M * I * 2;
+  if (lds > 96 * 1024) { set_error("down: %lld bytes of gathered rows exceed 96 KB (M=%lld, I=%lld)", (long long)lds, (long long)M, (long long)I); return kErrUnsupported; }
+  const void* fn = dense ? reinterpret_cast<const void*>(ref_down_kernel<true>) : reinterpret_cast<const void*>(ref_down_kernel<false>);
+  if (int rc = allow_dynamic_lds(fn, 96 * 1024, "down")) return rc;
+  if (dense)
+    hipLaunchKernelGGL(ref_down_kernel<true>, dim3(D / 16), dim3(kRefWaves * 64), static_cast<size_t>(lds), st,
+                       (const uint16_t*)h, (const uint8_t*)w2, s2, idx, probs, (const uint16_t*)x_in, (int)M, (int)P,
+                       (int)topk, (int)n_local, (int)D, (int)I, (uint16_t*)y);
+  else
+    hipLaunchKernelGGL(ref_down_kernel<false>, dim3(D / 16), dim3(kRefWaves * 64), static_cast<size_t>(lds), st,
+                       (const uint16_t*)h, (const uint8_t*)w2, s2, idx, probs, (const uint16_t*)x_in, (int)M, (int)P,
+                       (int)topk, (int)n_local, (int)D, (int)I, (uint16_t*)y);
+  return check_launch("down");
+}
+
+static int check_routing(const char* who, int64_t M, int64_t n_routed, int64_t topk, int64_t n_groups, int64_t topk_groups) {
+  if (M < 1 || M > 65535) { set_error("%s: M=%lld out of range", who, (long long)M); return kErrArg; }
+  if (n_routed < 1 || n_routed > kRefMaxRouted) { set_error("%s: n_routed=%lld must be in [1, %d]", who, (long long)n_routed, kRefMaxRouted); return kErrUnsupported; }
+  if (n_groups < 1 || n_groups > 64 || n_routed % n_groups) { set_error("%s: n_groups=%lld must divide n_routed=%lld (<= 64 groups)", who, (long long)n_groups, (long long)n_routed); return kErrArg; }
+  if (topk_groups < 1 || topk_groups > n_groups) { set_error("%s: topk_groups=%lld must be in [1, n_groups]", who, (long long)topk_groups); return kErrArg; }
+  if (topk < 1 || topk > 64 || topk > topk_groups * (n_routed / n_groups)) { set_error("%s: topk=%lld exceeds the experts of the kept groups", who, (long long)topk); return kErrArg; }
+  return kOk;
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+extern "C" int tl_moe_route(const float* scores, const float* bias, int64_t M, int64_t n_routed, int64_t topk,
+                            int64_t n_groups, int64_t topk_groups, float route_scale, float* probs_out, int32_t* idx_out,
+                            void* stream) {
+  if (int rc = check_routing("moe_route", M, n_routed, topk, n_groups, topk_groups)) return rc;
+  if (!scores || !probs_out || !idx_out) { set_error("moe_route: null pointer"); return kErrArg; }
+  hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(M)), dim3(64), 0, (hipStream_t)stream, scores, bias,
+                     (int)n_routed, (int)topk, (int)n_groups, (int)topk_groups, route_scale, probs_out, idx_out);
+  return check_launch("moe_route");
+}
+
+extern "C" int tl_expert_select_up_gate_silu(const void* x_bf16, const float* scores, const float* bias,
+                                             const void* w13_packed, const float* s13, int64_t M, int64_t n_routed,
+                                             int64_t topk, int64_t n_groups, int64_t topk_groups, float route_scale,
+                                             int64_t D, int64_t I, void* h_bf16, float* probs_out, int32_t* idx_out,
+                                             void* stream) {
+  const char* who = "expert_select_up_gate_silu";
+  if (int rc = check_routing(who, M, n_routed, topk, n_groups, topk_groups)) return rc;
+  if (int rc = check_common(who, M, 1 + topk, D, I)) return rc;
+  if (!x_bf16 || !scores || !w13_packed || !s13 || !h_bf16 || !probs_out || !idx_out) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed) | reinterpret_cast<uintptr_t>(h_bf16)) & 15) {
+    set_error("%s: x, weights and hidden_out must be 16-byte aligned", who);
+    return kErrArg;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(M)), dim3(64), 0, st, scores, bias, (int)n_routed,
+                     (int)topk, (int)n_groups, (int)topk_groups, route_scale, probs_out, idx_out);
+  if (int rc = check_launch(who)) return rc;
+  return launch_gate_up(false, x_bf16, nullptr, 0.f, w13_packed, s13, idx_out, M, 1 + topk, topk, 1 + n_routed, D, I,
+                        h_bf16, st);
+}
+
+extern "C" int tl_expert_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const int32_t* idx,
+                                        const float* probs, const void* x_in_bf16, int64_t M, int64_t n_routed,
+                                        int64_t topk, int64_t D, int64_t I, void* y_bf16, void* stream) {
+  const char* who = "expert_down_allreduce";
+  if (n_routed < 1 || n_routed + 1 > kRefMaxLocal) { set_error("%s: n_routed=%lld out of range", who, (long long)n_routed); return kErrUnsupported; }
+  if (topk < 1) { set_error("%s: topk must be positive", who); return kErrArg; }
+  if (int rc = check_common(who, M, 1 + topk, D, I)) return rc;
+  if (!h_bf16 || !w2_packed || !s2 || !idx || !probs || !y_bf16) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15 || reinterpret_cast<uintptr_t>(y_bf16) & 7 ||
+      reinterpret_cast<uintptr_t>(x_in_bf16) & 7) {
+    set_error("%s: h and weights must be 16-byte aligned, y and x_in 8-byte aligned", who);
+    return kErrArg;
+  }
+  return launch_down(false, h_bf16, w2_packed, s2, idx, probs, x_in_bf16, M, 1 + topk, topk, 1 + n_routed, D, I, y_bf16,
+                     (hipStream_t)stream);
+}
+
+extern "C" int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, float eps, const void* w13_packed,
+                                       const float* s13, int64_t M, int64_t n_chunks, int64_t D, int64_t I, void* h_bf16,
+                                       void* stream) {
+  const char* who = "rmsnorm_up_gate_silu";
+  if (n_chunks < 1 || n_chunks > kRefMaxLocal) { set_error("%s: n_chunks=%lld out of range", who, (long long)n_chunks); return kErrArg; }
+  if (int rc = check_common(who, M, n_chunks, D, I)) return rc;
+  if (M > 16) { set_error("%s: M=%lld > 16", who, (long long)M); return kErrUnsupported; }
+  if (!x_bf16 || !gamma || !w13_packed || !s13 || !h_bf16) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed) | reinterpret_cast<uintptr_t>(gamma) |
+       reinterpret_cast<uintptr_t>(h_bf16)) & 15) {
+    set_error("%s: x, gamma, weights and hidden_out must be 16-byte aligned", who);
+    return kErrArg;
+  }
+  return launch_gate_up(true, x_bf16, gamma, eps, w13_packed, s13, nullptr, M, n_chunks, 0, n_chunks, D, I, h_bf16,
+                        (hipStream_t)stream);
+}
+
+extern "C" int tl_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const void* x_in_bf16, int64_t M,
+                                 int64_t n_chunks, int64_t D, int64_t I, void* y_bf16, void* stream) {
+  const char* who = "down_allreduce";
+  if (n_chunks < 1 || n_chunks > kRefMaxLocal) { set_error("%s: n_chunks=%lld out of range", who, (long long)n_chunks); return kErrArg; }
+  if (int rc = check_common(who, M, n_chunks, D, I)) return rc;
+  if (!h_bf16 || !w2_packed || !s2 || !y_bf16) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15 || reinterpret_cast<uintptr_t>(y_bf16) & 7 ||
+      reinterpret_cast<uintptr_t>(x_in_bf16) & 7) {
+    set_error("%s: h and weights must be 16-byte aligned, y and x_in 8-byte aligned", who);
+    return kErrArg;
+  }
+  return launch_down(true, h_bf16, w2_packed, s2, nullptr, nullptr, x_in_bf16, M, n_chunks, 0, n_chunks, D, I, y_bf16,
+                     (hipStream_t)stream);
+}

@@ -1,14 +1,15 @@
-"""MoE expert layer at one expert-parallel shard, on the gfx950 HIP kernels.
-
-Mirrors the two reference ops of the routed-expert path:
-  * ``expert_select_up_gate_silu`` (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:23-48):
-    grouped gate/up GEMM + SwiGLU for the selected experts;
-  * ``expert_down_allreduce`` (deepseek_v3_2/ops/expert_down_allreduce.py:23-63): grouped
-    down GEMM + routing-weighted sum (+ the cross-GPU allreduce, which a single shard
-    does not need: its output is the shard's partial sum).
-Routing (sigmoid/bias/group-limited top-k, the ``scores_in``/``bias_in`` inputs of the
-reference op) is an input here: callers pass ``expert_indices`` [M, topk] int32 and
-``expert_probs`` [M, topk] fp32.
+"""MoE expert layer at one expert-parallel shard (32 local experts of
+256, whole experts per GPU), on the gfx950 HIP kernels:
+  * ``ep_gate_up_swiglu``: grouped gate/up GEMM + SwiGLU for the shard's hit experts (the
+    grouped GEMM of expert_select_up_gate_silu_op, deepseek_v3_2/ops/
+    expert_sel_up_gate_silu.py:23-48, golden :670-692);
+  * ``ep_down_combine``: grouped down GEMM + routing-weighted sum (expert_down_allreduce_op,
+    deepseek_v3_2/ops/expert_down_allreduce.py:23-63, golden :455-468) without the
+    cross-GPU sum: the output is the shard's partial.
+Routing is an input here (``expert_indices`` [M, topk] int32, ``expert_probs`` [M, topk]
+fp32).  The reference's own operators -- routing on the device, the shared expert, the
+tensor-parallel expert layout -- are ``tilert_amd.expert_sel_up_gate_silu`` and
+``tilert_amd.expert_down_allreduce``.
 """
 from __future__ import annotations
 
@@ -20,7 +21,8 @@ from .kernel import _require_cuda, _stream
 BLOCK = 128
 
 
-def _pack(w: torch.Tensor) -> torch.Tensor:
+def pack_moe_weight(w: torch.Tensor) -> torch.Tensor:
+    """Tile-major fragment packing of stacked per-expert weights [rows, K] (tl_moe_pack_weight)."""
     rows, K = w.shape
     out = torch.empty(rows * K, dtype=torch.uint8, device=w.device)
     _lib.call("tl_moe_pack_weight", w.data_ptr(), out.data_ptr(), rows, K, _stream(w))
@@ -47,8 +49,8 @@ class LocalExperts:
         self.n_local, self.I, self.D, self.expert_begin = E, I, D, expert_begin
         w13 = torch.cat([gate, up], dim=1).reshape(E * 2 * I, D).contiguous()
         self.s13 = torch.cat([gate_s, up_s], dim=1).float().contiguous()
-        self.w13 = _pack(w13)
-        self.w2 = _pack(down.reshape(E * D, I).contiguous())
+        self.w13 = pack_moe_weight(w13)
+        self.w2 = pack_moe_weight(down.reshape(E * D, I).contiguous())
         self.s2 = down_s.float().contiguous()
 
     @property
@@ -71,7 +73,7 @@ def _routing(idx: torch.Tensor, M: int) -> torch.Tensor:
     return idx
 
 
-def expert_select_up_gate_silu(hidden_in: torch.Tensor, expert_indices: torch.Tensor,
+def ep_gate_up_swiglu(hidden_in: torch.Tensor, expert_indices: torch.Tensor,
                                experts: LocalExperts, hidden_out: torch.Tensor | None = None,
                                profile_logs: torch.Tensor | None = None,
                                algorithm: str = "bf16mma", *, model_arch: str = "deepseek_v3_2"
@@ -93,14 +95,14 @@ def expert_select_up_gate_silu(hidden_in: torch.Tensor, expert_indices: torch.Te
     elif hidden_out.dtype != torch.bfloat16 or hidden_out.numel() < experts.n_local * M * experts.I \
             or not hidden_out.is_contiguous():
         raise ValueError("hidden_out must be a contiguous bf16 tensor of n_local*M*I elements")
-    _require_cuda("expert_select_up_gate_silu", x, idx, experts.w13, experts.s13, hidden_out)
+    _require_cuda("ep_gate_up_swiglu", x, idx, experts.w13, experts.s13, hidden_out)
     _lib.call("tl_moe_gate_up_swiglu", x.data_ptr(), experts.w13.data_ptr(), experts.s13.data_ptr(),
               idx.data_ptr(), M, idx.shape[1], experts.expert_begin, experts.n_local, experts.D,
               experts.I, hidden_out.data_ptr(), _stream(x))
     return hidden_out
 
 
-def expert_down_allreduce(vec_in: torch.Tensor, experts: LocalExperts, indices: torch.Tensor,
+def ep_down_combine(vec_in: torch.Tensor, experts: LocalExperts, indices: torch.Tensor,
                           scores: torch.Tensor, x_in: torch.Tensor | None = None, flag: int = 0,
                           vec_out: torch.Tensor | None = None,
                           profile_logs: torch.Tensor | None = None,
@@ -109,7 +111,7 @@ def expert_down_allreduce(vec_in: torch.Tensor, experts: LocalExperts, indices: 
     """Down GEMM + routing-weighted combine for this shard (argument order of the reference
     op; ``mat_in``/``mat_scale`` are carried by ``experts``).
 
-    vec_in bf16 [n_local, M, I] from ``expert_select_up_gate_silu``; indices int32 and
+    vec_in bf16 [n_local, M, I] from ``ep_gate_up_swiglu``; indices int32 and
     scores fp32 [M, topk].  Returns vec_out bf16 [M, D].  ``x_in``/``flag`` belong to the
     cross-GPU allreduce epilogue, which one shard does not run (the reference's
     single-GPU golden, padded_allreduce_add.py:100-114, is the identity); they are
@@ -131,7 +133,7 @@ def expert_down_allreduce(vec_in: torch.Tensor, experts: LocalExperts, indices: 
         vec_out = torch.empty(M, experts.D, dtype=torch.bfloat16, device=vec_in.device)
     elif vec_out.dtype != torch.bfloat16 or vec_out.numel() != M * experts.D or not vec_out.is_contiguous():
         raise ValueError("vec_out must be a contiguous bf16 tensor of M*D elements")
-    _require_cuda("expert_down_allreduce", vec_in, idx, w, experts.w2, experts.s2, vec_out)
+    _require_cuda("ep_down_combine", vec_in, idx, w, experts.w2, experts.s2, vec_out)
     _lib.call("tl_moe_down_combine", vec_in.data_ptr(), experts.w2.data_ptr(), experts.s2.data_ptr(),
               idx.data_ptr(), w.data_ptr(), M, idx.shape[1], experts.expert_begin, experts.n_local,
               experts.D, experts.I, vec_out.data_ptr(), _stream(vec_in))
@@ -142,5 +144,5 @@ def moe_forward(x: torch.Tensor, experts: LocalExperts, expert_indices: torch.Te
                 expert_probs: torch.Tensor, h_buf: torch.Tensor | None = None,
                 out: torch.Tensor | None = None) -> torch.Tensor:
     """The shard's routed-expert layer: gate/up + SwiGLU, down, weighted combine."""
-    h = expert_select_up_gate_silu(x, expert_indices, experts, h_buf)
-    return expert_down_allreduce(h, experts, expert_indices, expert_probs, vec_out=out)
+    h = ep_gate_up_swiglu(x, expert_indices, experts, h_buf)
+    return ep_down_combine(h, experts, expert_indices, expert_probs, vec_out=out)
