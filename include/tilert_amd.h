@@ -30,6 +30,8 @@
  *   tl_expert_select_up_gate_silu  expert_select_up_gate_silu_op  .../ops/expert_sel_up_gate_silu.py:23-48
  *   tl_expert_down_allreduce       expert_down_allreduce_op       .../ops/expert_down_allreduce.py:23-63
  *                          (these two: the reference's own tensor-parallel layout, shared expert)
+ *   tl_head_gemm_bf16        projq_wqb_op / projo_wkvb_op / unproj_o_allreduce_op
+ *                            .../ops/projq_wqb.py:24-54, projo_wkvb.py:24-54, unproj_o_allreduce.py:23-58
  *   tl_rmsnorm_up_gate_silu  rmsnorm_up_gate_silu_op  .../ops/rmsnorm_up_gate_silu.py:26-44
  *   tl_down_allreduce        down_allreduce_op        .../ops/down_allreduce.py:24-59
  *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
@@ -242,6 +244,19 @@ int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, float eps, c
  * h bf16 [M, n_chunks, I], y bf16 [M, D]. */
 int tl_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const void* x_in_bf16,
                       int64_t M, int64_t n_chunks, int64_t D, int64_t I, void* y_bf16, void* stream);
+
+/* Per-head bf16 x fp8 GEMV: y[t, h, :] = bf16(x[t, h, :] . W_h^T) for H weights W_h [N, K]
+ * (bf16 activations times bf16(fp32(q) * block scale) weights, fp32 accumulation), and
+ * y = bf16(y + x_in) when x_in bf16 [M, H, N] is given.  x bf16 [M, H, K] (M*H*K*2 <= 64 KB),
+ * w_packed = tl_moe_pack_weight of the stacked [H * N, K] weights, w_s fp32
+ * [H, ceil(N/128), K/128], y bf16 [M, H, N]; N % 16 == 0, K % 128 == 0, M <= 16.  The absorbed
+ * MLA projections at one device's share: projq_wqb_op (.../ops/projq_wqb.py:24-54, golden
+ * :448-450; each head's [128, kv_lora] nope block of wkv_b stored transposed), projo_wkvb_op
+ * (.../ops/projo_wkvb.py:24-54, golden :465-467) and, with H = 1 and the residual,
+ * unproj_o_allreduce_op (.../ops/unproj_o_allreduce.py:23-58, golden :480-498; the single-GPU
+ * form of its allreduce epilogue). */
+int tl_head_gemm_bf16(const void* x_bf16, const void* w_packed, const float* w_s, const void* x_in_bf16,
+                      int64_t M, int64_t H, int64_t N, int64_t K, void* y_bf16, void* stream);
 
 /* RMSNorm with optional activation quantisation (rmsnorm_quant_op / rmsnorm_op,
  * ops/rmsnorm_quant.py:19-63; norm of tilert/models/common.py:92-133 without residual).

@@ -520,3 +520,44 @@ def down_allreduce(h: torch.Tensor, dq: torch.Tensor, ds: torch.Tensor, bf16_wei
     if x_in is not None:
         y = (y.float() + x_in.float()).to(torch.bfloat16)
     return y
+
+
+# ------------------------------------------------------ absorbed MLA projections
+def _kv_b_heads(wkv_b: torch.Tensor, s: torch.Tensor, n_heads: int, bf16_weights: bool) -> torch.Tensor:
+    w = weight_dequant(wkv_b, s)
+    if bf16_weights:
+        w = w.to(torch.bfloat16).float()
+    return w.view(n_heads, -1, w.shape[-1])
+
+
+def projq_wqb(q_nope: torch.Tensor, wkv_b: torch.Tensor, s: torch.Tensor, n_heads: int, nope_dim: int,
+              bf16_weights: bool) -> torch.Tensor:
+    """``ProjqWqb.golden_forward`` (deepseek_v3_2/ops/projq_wqb.py:448-450, weights from
+    ``init_reference_weights`` :374-385): the device's kv_b_proj shard dequantised, viewed
+    [heads, nope + v, kv_lora], its first nope rows per head; ``einsum("bshd,hdc->bshc")`` in
+    fp32 -> bf16.  ``bf16_weights`` rounds the dequantised weights to bf16 (bf16 inference's
+    default dtype, the kernel's numerics)."""
+    w = _kv_b_heads(wkv_b, s, n_heads, bf16_weights)[:, :nope_dim]
+    return torch.einsum("bshd,hdc->bshc", q_nope.float(), w).to(torch.bfloat16)
+
+
+def projo_wkvb(o_lat: torch.Tensor, wkv_b: torch.Tensor, s: torch.Tensor, n_heads: int, v_dim: int,
+               bf16_weights: bool) -> torch.Tensor:
+    """``ProjoWKVb.golden_forward`` (deepseek_v3_2/ops/projo_wkvb.py:465-467, weights :390-400):
+    each head's last v_dim rows; ``einsum("bshc,hdc->bshd")`` in fp32 -> bf16."""
+    w = _kv_b_heads(wkv_b, s, n_heads, bf16_weights)[:, -v_dim:]
+    return torch.einsum("bshc,hdc->bshd", o_lat.float(), w).to(torch.bfloat16)
+
+
+def unproj_o_allreduce(vec_in: torch.Tensor, wo: torch.Tensor, s: torch.Tensor, bf16_weights: bool,
+                       x_in: torch.Tensor | None = None) -> torch.Tensor:
+    """``UnProjOAllReduce.golden_forward`` (deepseek_v3_2/ops/unproj_o_allreduce.py:480-498):
+    vec_in [1, s, ...] flattened per token, fp32 @ the dequantised o_proj shard^T -> bf16;
+    + x_in as in ``expert_down_allreduce``."""
+    w = weight_dequant(wo, s)
+    if bf16_weights:
+        w = w.to(torch.bfloat16).float()
+    y = (vec_in.reshape(vec_in.shape[0], vec_in.shape[1], -1).float() @ w.T).to(torch.bfloat16)
+    if x_in is not None:
+        y = (y.float() + x_in.float()).to(torch.bfloat16)
+    return y

@@ -481,3 +481,28 @@ def test_dense_mlp_goldens_vs_fp64_and_variants():
     y = ref.down_allreduce(h16, *W["down"], bf16_weights=False)
     acc = sum(h16[:, i].double() @ ref.weight_dequant(*[w[i] for w in W["down"]]).double().T for i in range(C))
     assert torch.allclose(y.double(), acc, rtol=2e-2, atol=2e-2)
+
+
+# -------------------------------------------------------- absorbed MLA projections
+def test_absorbed_mla_goldens_vs_fp64_loops():
+    g = synth.gen(47)
+    H, nope, v, kv, T = 3, 128, 128, 256, 2
+    wq, ws = ref.weight_quant(synth.weight_fp32(H * (nope + v), kv, g))
+    wd = ref.weight_dequant(wq, ws).double()
+    q = synth.activations(T, H * nope, g).reshape(1, T, H, nope)
+    o = synth.activations(T, H * kv, g).reshape(1, T, H, kv)
+    ql = ref.projq_wqb(q, wq, ws, H, nope, bf16_weights=False)
+    ov = ref.projo_wkvb(o, wq, ws, H, v, bf16_weights=False)
+    for t in range(T):
+        for h in range(H):
+            blk = wd[h * (nope + v):(h + 1) * (nope + v)]
+            want_q = sum(q[0, t, h, d].double() * blk[d] for d in range(nope))  # rows contracted
+            assert torch.allclose(ql[0, t, h].double(), want_q, rtol=1e-2, atol=1e-3)
+            want_o = blk[nope:] @ o[0, t, h].double()  # columns contracted
+            assert torch.allclose(ov[0, t, h].double(), want_o, rtol=1e-2, atol=1e-3)
+    wo, wos = ref.weight_quant(synth.weight_fp32(256, H * v, g))
+    xin = synth.activations(T, 256, g).reshape(1, T, 256)
+    x = synth.activations(T, H * v, g).reshape(1, T, H, v)
+    y = ref.unproj_o_allreduce(x, wo, wos, bf16_weights=False, x_in=xin)
+    want = x.reshape(T, -1).double() @ ref.weight_dequant(wo, wos).double().T + xin[0].double()
+    assert torch.allclose(y[0].double(), want, rtol=2e-2, atol=2e-2)

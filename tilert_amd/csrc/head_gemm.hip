@@ -1,0 +1,120 @@
+// Per-head bf16 x fp8 GEMV: y[t, h, :] = x[t, h, :] . W_h^T for H independent weights
+// W_h [N, K] (fp8 e4m3fn, 128x128 block scales), with an optional residual.  It carries
+// three operators of the absorbed MLA attention at one device's share (DeepSeek-V3.2 /
+// GLM-5, 16 local heads):
+//  * projq_wqb (deepseek_v3_2/ops/projq_wqb.py:24-54, golden :448-450): q_lat[t,h,:] =
+//    q_nope[t,h,:] . wkv_b[h, :128, :] -- the weight's ROWS are contracted, so the converter
+//    stores each head's nope block transposed (N = kv_lora_rank 512, K = 128);
+//  * projo_wkvb (.../projo_wkvb.py:24-54, golden :465-467): o[t,h,:] = o_lat[t,h,:] .
+//    wkv_b[h, 128:, :]^T (N = v_head_dim 128, K = 512);
+//  * unproj_o_allreduce (.../unproj_o_allreduce.py:23-58, golden :480-498): H = 1,
+//    y = o_flat . wo_shard^T (N = dim, K = local heads * 128) + the residual x_in.
+// Numerics: bf16 activations times the block-dequantised weights rounded to bf16 (the
+// goldens' weights in bf16 inference), v_mfma_f32_16x16x32_bf16, fp32 accumulation, bf16
+// output; with a residual, bf16(bf16(y) + x_in).
+//
+// Layout: W is the tile-major fragment packing of tl_moe_pack_weight applied to the
+// stacked [H * N, K] matrix; scales fp32 [H][N/128][K/128].  A workgroup stages x [M, H, K]
+// in LDS once; work item = (head, 16-row tile) over a persistent grid; its waves take the
+// K blocks round-robin (two in flight each) and are reduced through LDS in wave order.
+#include <algorithm>
+
+#include "common.h"
+#include "moe_common.h"
+#include "../../include/tilert_amd.h"
+
+namespace tl {
+
+constexpr int kHgMaxWaves = 8;
+constexpr int kHgLdsX = 64 * 1024;
+
+__global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ s,
+    const uint16_t* __restrict__ x_in, int M, int H, int N, int K, uint16_t* __restrict__ y) {
+  extern __shared__ __align__(16) uint16_t xl[];  // [M][H][K]
+  __shared__ float red[kHgMaxWaves - 1][4][64];
+  const int lane = threadIdx.x & 63;
+  const int nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int x16 = M * H * K / 8;
+  for (int c = threadIdx.x; c < x16; c += blockDim.x)
+    reinterpret_cast<u32x4*>(xl)[c] = reinterpret_cast<const u32x4*>(x)[c];
+  __syncthreads();
+  const int KB = K >> 7, tiles = N >> 4, SB = (N + 127) >> 7;
+  const int r = lane & 15, g = lane >> 4;
+  const int row = min(r, M - 1);
+  const int n = wave < KB ? (KB - wave + nw - 1) / nw : 0;  // K blocks wave + i * nw
+  for (int item = blockIdx.x; item < H * tiles; item += gridDim.x) {
+    const int h = item / tiles, rt = item - h * tiles;
+    const uint8_t* wt = w + (static_cast<size_t>(h) * tiles + rt) * KB * 2048;
+    const float* st = s + (static_cast<size_t>(h) * SB + ((rt * 16) >> 7)) * KB;
+    const uint16_t* xr = xl + (static_cast<size_t>(row) * H + h) * K;
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+    struct Ops {
+      v8i w;
+      float sc;
+    };
+    Ops buf[2];
+    ring_pipeline(
+        n, buf,
+        [&](int i, Ops& o) {
+          const int kb = wave + i * nw;
+          o.w = load_fragment(wt + static_cast<size_t>(kb) * 2048, lane);
+          o.sc = load_f32_vector(st + kb);
+        },
+        [&](int i, const Ops& o) {
+          const int kb = wave + i * nw;
+          acc = mfma_block_bf16(o.w, o.sc, lds_act(xr + kb * kBlock, g), acc);
+        });
+    if (wave > 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave - 1][q][lane] = acc[q];
+    }
+    __syncthreads();
+    if (wave == 0 && r < M) {
+      for (int ww = 0; ww < nw - 1; ++ww)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] += red[ww][q][lane];
+      const size_t off = (static_cast<size_t>(r) * H + h) * N + rt * 16 + 4 * g;
+      uint16_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        o[q] = f32_to_bf16(acc[q]);
+        if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(x_in[off + q]));
+      }
+      *reinterpret_cast<uint2*>(y + off) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
+                                                      o[2] | (static_cast<uint32_t>(o[3]) << 16));
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace tl
+
+using namespace tl;
+
+extern "C" int tl_head_gemm_bf16(const void* x_bf16, const void* w_packed, const float* w_s, const void* x_in_bf16,
+                                 int64_t M, int64_t H, int64_t N, int64_t K, void* y_bf16, void* stream) {
+  const char* who = "head_gemm_bf16";
+  if (M < 1 || M > 16 || H < 1 || H > 1024) { set_error("%s: M=%lld must be in [1, 16], H=%lld in [1, 1024]", who, (long long)M, (long long)H); return kErrUnsupported; }
+  if (N <= 0 || K <= 0 || N % 16 || K % kBlock || N > (1 << 20) || K > (1 << 16)) {
+    set_error("%s: N=%lld must be a positive multiple of 16 and K=%lld of 128", who, (long long)N, (long long)K);
+    return kErrArg;
+  }
+  const int64_t x_bytes = M * H * K * 2;
+  if (x_bytes > kHgLdsX) { set_error("%s: x of %lld bytes exceeds %d", who, (long long)x_bytes, kHgLdsX); return kErrUnsupported; }
+  if (!x_bf16 || !w_packed || !w_s || !y_bf16) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w_packed)) & 15 ||
+      (reinterpret_cast<uintptr_t>(y_bf16) | reinterpret_cast<uintptr_t>(x_in_bf16)) & 7) {
+    set_error("%s: x and weights must be 16-byte aligned, y and x_in 8-byte aligned", who);
+    return kErrArg;
+  }
+  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(head_gemm_kernel), kHgLdsX, who)) return rc;
+  const int64_t items = H * (N / 16);
+  const int waves = static_cast<int>(std::min<int64_t>(kHgMaxWaves, std::max<int64_t>(K / kBlock, 1)));
+  const int grid = static_cast<int>(std::min<int64_t>(items, 512));
+  hipLaunchKernelGGL(head_gemm_kernel, dim3(grid), dim3(waves * 64), static_cast<size_t>(x_bytes), (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, (const uint8_t*)w_packed, w_s, (const uint16_t*)x_in_bf16, (int)M, (int)H,
+                     (int)N, (int)K, (uint16_t*)y_bf16);
+  return check_launch(who);
+}
