@@ -32,6 +32,9 @@
  *                          (these two: the reference's own tensor-parallel layout, shared expert)
  *   tl_head_gemm_bf16        projq_wqb_op / projo_wkvb_op / unproj_o_allreduce_op
  *                            .../ops/projq_wqb.py:24-54, projo_wkvb.py:24-54, unproj_o_allreduce.py:23-58
+ *   tl_projx_wqaki           projx_wqaki_op           .../ops/projx_wqaki.py:11-44
+ *   tl_bf16_gemv             proj_w_op (projx_wis)    .../ops/projx_wis.py:18-37
+ *   tl_rmsnorm_projq_wqb with rope_dim = 0: rmsnorm_proj_qi_op  .../ops/rmsnorm_projq_wqi.py:17-37
  *   tl_rmsnorm_up_gate_silu  rmsnorm_up_gate_silu_op  .../ops/rmsnorm_up_gate_silu.py:26-44
  *   tl_down_allreduce        down_allreduce_op        .../ops/down_allreduce.py:24-59
  *   tl_rmsnorm_quant       rmsnorm_quant_op / rmsnorm_op  .../ops/rmsnorm_quant.py:19-63
@@ -258,6 +261,23 @@ int tl_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2
 int tl_head_gemm_bf16(const void* x_bf16, const void* w_packed, const float* w_s, const void* x_in_bf16,
                       int64_t M, int64_t H, int64_t N, int64_t K, void* y_bf16, void* stream);
 
+/* The indexer's fused query/key down-projection, projx_wqaki_op
+ * (deepseek_v3_2/ops/projx_wqaki.py:11-44): x_q . [wq_a; wk]^T in one FP8 GEMV launch, columns
+ * [0, q_rank) -> q_out bf16 [M, q_rank], the rest -> ki_out bf16 [M, ki_dim].  w_packed =
+ * tl_fp8_pack_weight of the row-stacked [q_rank + ki_dim, dim] weight, w_s its fp32 block
+ * scales (wq_a's rows, then wk's; q_rank % 128 == 0).  M <= 64, dim % 512 == 0; workspace
+ * as tl_fp8_gemm_workspace_bytes(M, q_rank + ki_dim, dim). */
+int tl_projx_wqaki(const void* x_q, const float* x_s, const void* w_packed, const float* w_s, void* q_out,
+                   void* ki_out, int64_t M, int64_t dim, int64_t q_rank, int64_t ki_dim, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
+/* y bf16 [M, N] = bf16(x . w^T) with bf16 x [M, K] and bf16 weights w [N, K] (row-major),
+ * fp32 accumulation: proj_w_op, the indexer head-weight projection of projx_wis
+ * (deepseek_v3_2/ops/projx_wis.py:18-37; golden RMSNormProjxWqakis :289-299).  M <= 16,
+ * N % 16 == 0, K % 128 == 0, K <= 8192. */
+int tl_bf16_gemv(const void* x_bf16, const void* w_bf16, int64_t M, int64_t N, int64_t K, void* y_bf16,
+                 void* stream);
+
 /* RMSNorm with optional activation quantisation (rmsnorm_quant_op / rmsnorm_op,
  * ops/rmsnorm_quant.py:19-63; norm of tilert/models/common.py:92-133 without residual).
  * x bf16 [rows, dim], gamma fp32 [dim]: y_bf16 = bf16(gamma * x * 1/sqrt(mean(x^2) + eps))
@@ -306,7 +326,9 @@ int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t 
  * q_nope [M, heads, nope_dim] and q_pe [M, heads, rope_dim] (feature h * (nope + rope) + d
  * of the weight is head h, dim d).  wq_b_packed: the [heads * (nope + rope), q_rank] e4m3fn
  * weight in tl_fp8_pack_weight's layout; wq_b_s its fp32 [N/128, q_rank/128] scales.
- * 1 <= M <= 16, q_rank % 512 == 0 and <= 2048, nope/rope multiples of 16. */
+ * 1 <= M <= 16, q_rank % 512 == 0 and <= 2048, nope/rope multiples of 16.  rope_dim = 0 sends
+ * every feature to q_nope (q_pe may be null): rmsnorm_proj_qi_op, the indexer's query
+ * projection (ops/rmsnorm_projq_wqi.py:17-37, golden :301-314), heads = 64, nope = 128. */
 int tl_rmsnorm_projq_wqb(const void* q_bf16, const float* q_norm_weight, float eps, const void* wq_b_packed,
                          const float* wq_b_s, void* q_nope_bf16, void* q_pe_bf16, int64_t M, int64_t heads,
                          int64_t q_rank, int64_t nope_dim, int64_t rope_dim, void* stream);

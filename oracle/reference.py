@@ -561,3 +561,31 @@ def unproj_o_allreduce(vec_in: torch.Tensor, wo: torch.Tensor, s: torch.Tensor, 
     if x_in is not None:
         y = (y.float() + x_in.float()).to(torch.bfloat16)
     return y
+
+
+# ------------------------------------------------------ the indexer's projections
+def rmsnorm_projq_wqi(q: torch.Tensor, gamma: torch.Tensor, wqi: torch.Tensor, wqi_s: torch.Tensor, n_heads: int,
+                      head_dim: int = 128, eps: float = 1e-6) -> torch.Tensor:
+    """``RmsnormProjqWqi.golden_forward`` (deepseek_v3_2/ops/rmsnorm_projq_wqi.py:301-314):
+    qr = bf16(rms_norm(q fp32, gamma, eps)); iq = qr @ bf16(dequant(wqi))^T viewed
+    [..., n_heads, head_dim] -- ``rmsnorm_projq_wqb`` with no rope split."""
+    iq, _ = rmsnorm_projq_wqb(q, gamma, wqi, wqi_s, n_heads, head_dim, 0, eps)
+    return iq
+
+
+def projx_wis(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``proj_w_op`` as the decoupled module runs it (rmsnorm_projx_wqakis.py:325-333): the
+    bf16 normalised rows times the bf16 weights_proj^T, fp32 accumulation -> bf16."""
+    return (x.float() @ w.float().T).to(torch.bfloat16)
+
+
+def rmsnorm_projx_wqakis(x: torch.Tensor, gamma: torch.Tensor, wq_a: torch.Tensor, wq_a_s: torch.Tensor,
+                         wk: torch.Tensor, wk_s: torch.Tensor, wis: torch.Tensor, eps: float = 1e-6):
+    """``RMSNormProjxWqakis.golden_forward`` (deepseek_v3_2/ops/rmsnorm_projx_wqakis.py:279-299):
+    fp32 rms_norm, then fp32 matmuls with the dequantised wq_a and wk and the bf16 weights_proj
+    -> (q, ki, idx_scores) bf16."""
+    xn = rms_norm_f32(x, gamma, eps)
+    q = (xn @ weight_dequant(wq_a, wq_a_s).T).to(torch.bfloat16)
+    ki = (xn @ weight_dequant(wk, wk_s).T).to(torch.bfloat16)
+    sc = (xn @ wis.float().T).to(torch.bfloat16)
+    return q, ki, sc

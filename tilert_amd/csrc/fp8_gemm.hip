@@ -1219,13 +1219,14 @@ extern "C" int tl_rmsnorm_projq_wqb(const void* q_bf16, const float* q_norm_weig
                                     int64_t q_rank, int64_t nope_dim, int64_t rope_dim, void* stream) {
   const int64_t N = heads * (nope_dim + rope_dim), K = q_rank;
   if (M < 1 || M > 16) { set_error("rmsnorm_projq_wqb: M=%lld must be in [1, 16]", (long long)M); return kErrUnsupported; }
-  if (heads < 1 || nope_dim <= 0 || rope_dim <= 0 || nope_dim % 16 || rope_dim % 16) {
+  // rope_dim = 0: every feature goes to q_nope (rmsnorm_proj_qi_op's single output)
+  if (heads < 1 || nope_dim <= 0 || rope_dim < 0 || nope_dim % 16 || rope_dim % 16) {
     set_error("rmsnorm_projq_wqb: heads=%lld, nope=%lld, rope=%lld (dims must be positive multiples of 16)",
               (long long)heads, (long long)nope_dim, (long long)rope_dim);
     return kErrArg;
   }
   if (K % (kBlock * kGroup) || K > kPqMaxKb * kBlock) { set_error("rmsnorm_projq_wqb: q_rank=%lld must be a multiple of 512 and <= %d", (long long)K, kPqMaxKb * kBlock); return kErrUnsupported; }
-  if (!q_bf16 || !q_norm_weight || !wq_b_packed || !wq_b_s || !q_nope_bf16 || !q_pe_bf16) { set_error("rmsnorm_projq_wqb: null pointer"); return kErrArg; }
+  if (!q_bf16 || !q_norm_weight || !wq_b_packed || !wq_b_s || !q_nope_bf16 || (rope_dim > 0 && !q_pe_bf16)) { set_error("rmsnorm_projq_wqb: null pointer"); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(q_bf16) | reinterpret_cast<uintptr_t>(wq_b_packed)) & 15 ||
       (reinterpret_cast<uintptr_t>(q_nope_bf16) | reinterpret_cast<uintptr_t>(q_pe_bf16)) & 7) {
     set_error("rmsnorm_projq_wqb: q and the weight must be 16-byte aligned, outputs 8-byte aligned");
@@ -1310,4 +1311,27 @@ extern "C" int tl_fp8_gemm_packed_static(const void* a, const float* a_s, const 
   }
   return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, plain_out((uint16_t*)c_bf16, (int)N),
                            (int)M, (int)N, (int)K, ws, (hipStream_t)stream);
+}
+
+extern "C" int tl_projx_wqaki(const void* x_q, const float* x_s, const void* w_packed, const float* w_s, void* q_out,
+                              void* ki_out, int64_t M, int64_t dim, int64_t q_rank, int64_t ki_dim, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  const char* who = "projx_wqaki";
+  if (M <= 0 || q_rank <= 0 || ki_dim <= 0) { set_error("%s: M and the output widths must be positive", who); return kErrArg; }
+  if (q_rank % kBlock || ki_dim % 16) {
+    set_error("%s: q_rank must be a multiple of 128 and ki_dim of 16 (got %lld, %lld)", who, (long long)q_rank, (long long)ki_dim);
+    return kErrArg;
+  }
+  if (dim % (kBlock * kGroup)) { set_error("%s: dim=%lld must be a multiple of 512", who, (long long)dim); return kErrArg; }
+  if (M > 64) { set_error("%s: M=%lld > 64 is not supported (decode GEMV)", who, (long long)M); return kErrUnsupported; }
+  if (!ki_out) { set_error("%s: null pointer", who); return kErrArg; }
+  if (reinterpret_cast<uintptr_t>(ki_out) & 7) { set_error("%s: outputs must be 8-byte aligned", who); return kErrArg; }
+  const int64_t N = q_rank + ki_dim;
+  const size_t need = tl_fp8_gemm_workspace_bytes(M, N, dim);
+  int rc = validate(who, x_q, x_s, w_packed, w_s, q_out, M, N, dim, workspace, workspace_bytes, need);
+  if (rc) return rc;
+  // two output segments: columns [0, q_rank) -> q_out, the rest -> ki_out
+  OutRoute out{(uint16_t*)q_out, (uint16_t*)ki_out, nullptr, (int)q_rank, (int)N, (int)q_rank, (int)ki_dim, 0, nullptr, 1, 0};
+  return launch_gemm<true>((const uint8_t*)x_q, x_s, (const uint8_t*)w_packed, w_s, out, (int)M, (int)N, (int)dim,
+                           workspace, (hipStream_t)stream);
 }

@@ -89,9 +89,79 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
   }
 }
 
+// ------------------------------------------------------------ bf16-weight GEMV
+// y[t, n] = bf16( sum_k x[t, k] * w[n, k] ), x and w bf16 row-major (no scales), fp32
+// accumulation on v_mfma_f32_16x16x32_bf16: proj_w_op, the indexer's head-weight projection
+// (deepseek_v3_2/ops/projx_wis.py:18-37; its weights_proj stays bf16, rmsnorm_projx_wqakis.py:38-41).
+// One workgroup of 16 waves per 16-row tile; wave w takes K blocks w, w + 16, ... -- up to
+// kBgBlocks of them, all requested before the first MFMA -- reduced through LDS in wave order.
+constexpr int kBgWaves = 16;
+constexpr int kBgBlocks = 4;  // K <= 16 * 4 * 128 = 8192
+
+__global__ __launch_bounds__(kBgWaves * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x,
+                                                                  const uint16_t* __restrict__ w, int M, int N, int K,
+                                                                  uint16_t* __restrict__ y) {
+  __shared__ float red[kBgWaves - 1][4][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int KB = K >> 7;
+  const int rt = blockIdx.x;
+  const uint16_t* wr = w + static_cast<size_t>(16 * rt + r) * K;
+  const uint16_t* xr = x + static_cast<size_t>(min(r, M - 1)) * K;
+  const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
+  v8bf wa[kBgBlocks][4], xa[kBgBlocks][4];
+#pragma unroll
+  for (int i = 0; i < kBgBlocks; ++i) {
+    const int kb = min(wave + i * kBgWaves, KB - 1);  // unconditional loads (clamped)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wa[i][j] = *reinterpret_cast<const v8bf*>(wr + kb * kBlock + off[j]);
+      xa[i][j] = *reinterpret_cast<const v8bf*>(xr + kb * kBlock + off[j]);
+    }
+  }
+  v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < kBgBlocks; ++i) {
+    if (wave + i * kBgWaves < KB) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i][j], xa[i][j], acc, 0, 0, 0);
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[wave - 1][q][lane] = acc[q];
+  }
+  __syncthreads();
+  if (wave == 0 && r < M) {
+    for (int ww = 0; ww < kBgWaves - 1; ++ww)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q] += red[ww][q][lane];
+    uint16_t* dst = y + static_cast<size_t>(r) * N + 16 * rt + 4 * g;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16),
+                                                f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16));
+  }
+}
+
 }  // namespace tl
 
 using namespace tl;
+
+extern "C" int tl_bf16_gemv(const void* x_bf16, const void* w_bf16, int64_t M, int64_t N, int64_t K, void* y_bf16,
+                            void* stream) {
+  const char* who = "bf16_gemv";
+  if (M < 1 || M > 16) { set_error("%s: M=%lld must be in [1, 16]", who, (long long)M); return kErrUnsupported; }
+  if (N <= 0 || N % 16 || K <= 0 || K % kBlock || N > (1 << 20)) { set_error("%s: N=%lld must be a positive multiple of 16 and K=%lld of 128", who, (long long)N, (long long)K); return kErrArg; }
+  if (K > kBgWaves * kBgBlocks * kBlock) { set_error("%s: K=%lld > %d", who, (long long)K, kBgWaves * kBgBlocks * kBlock); return kErrUnsupported; }
+  if (!x_bf16 || !w_bf16 || !y_bf16) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w_bf16)) & 15 || reinterpret_cast<uintptr_t>(y_bf16) & 7) {
+    set_error("%s: x and w must be 16-byte aligned, y 8-byte aligned", who);
+    return kErrArg;
+  }
+  hipLaunchKernelGGL(bf16_gemv_kernel, dim3(static_cast<unsigned>(N / 16)), dim3(kBgWaves * 64), 0, (hipStream_t)stream,
+                     (const uint16_t*)x_bf16, (const uint16_t*)w_bf16, (int)M, (int)N, (int)K, (uint16_t*)y_bf16);
+  return check_launch(who);
+}
 
 extern "C" int tl_head_gemm_bf16(const void* x_bf16, const void* w_packed, const float* w_s, const void* x_in_bf16,
                                  int64_t M, int64_t H, int64_t N, int64_t K, void* y_bf16, void* stream) {
