@@ -112,6 +112,25 @@ def test_topk_ties_across_chunks(cuda):
     assert out.tolist() == sorted(winners + ties)
 
 
+@pytest.mark.parametrize("rows,L,k", [(2, 131072, 2048), (1, 20000, 512)])
+def test_topk_unrepresentative_sample_falls_back_exactly(cuda, rows, L, k):
+    """The row's largest values sit exactly at the strided sample's positions, so the
+    sample's threshold admits fewer than k candidates: the whole-row selection must take
+    over and still return the exact set."""
+    g = synth.gen(rows + L)
+    x = torch.randn(rows, L, generator=g)
+    n = [L - rows + 1 + i for i in range(rows)]
+    for i in range(rows):
+        S = min(4096, n[i])
+        pos = torch.arange(S) * n[i] // S
+        x[i, pos] = 10.0 + torch.arange(S, dtype=torch.float32) * 1e-3
+    out = topk_rows(x.to(cuda), L - rows, k).cpu()
+    want = ref.topk_rows(x, n, k)
+    for i in range(rows):
+        assert torch.equal(out[i].sort().values, want[i].sort().values)
+    _assert_topk_set(out, x, n, k)
+
+
 def test_topk_repeatable(cuda):
     """The cross-workgroup handoff re-arms itself: repeated calls give the same set."""
     g = synth.gen(77)
