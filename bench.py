@@ -288,6 +288,97 @@ def bench_indexer(torch, steps, dev, cpu=True, keep=False):
     torch.cuda.empty_cache()
     return res
 
+def bench_ref_layout(torch, steps, dev):
+    """The reference's own operator layouts at one device's share (DeepSeek-V3.2, M = 4):
+    the tensor-parallel MoE (257 experts x 256 rows, routing on the device, residual), the
+    dense MLP's 9 chunks x 256, and the absorbed MLA projections (16 heads)."""
+    from tilert_amd.down_allreduce import down_allreduce
+    from tilert_amd.expert_down_allreduce import DownExperts, expert_down_allreduce
+    from tilert_amd.expert_sel_up_gate_silu import UpGateExperts, expert_select_up_gate_silu
+    from tilert_amd.projo_wkvb import convert_projo_wkvb, projo_wkvb
+    from tilert_amd.projq_wqb import convert_projq_wqb, projq_wqb
+    from tilert_amd.rmsnorm_up_gate_silu import rmsnorm_up_gate_silu
+    from tilert_amd.unproj_o_allreduce import convert_unproj_o, unproj_o_allreduce
+    out = {}
+    st = max(10, steps // 10)
+    M, D, I, E = 4, 7168, 256, 257
+    g = torch.Generator(device=dev).manual_seed(11)
+
+    def stack(n, k, cnt):
+        qs, ss = [], []
+        for _ in range(cnt):
+            q, s_ = K_.weight_quant(torch.randn(n, k, device=dev, generator=g) * 0.02)
+            qs.append(q)
+            ss.append(s_)
+        return torch.stack(qs), torch.stack(ss)
+    copies = []
+    for _ in range(2):  # 2 x 1.4 GB of expert weights: the MALL cannot hold a copy
+        copies.append((UpGateExperts(*stack(I, D, E), *stack(I, D, E)), DownExperts(*stack(D, I, E))))
+    gc = torch.Generator().manual_seed(12)
+    scores = [torch.randn(1, M, 256, generator=gc).to(dev) for _ in range(st)]
+    bias = (torch.randn(256, generator=gc) * 0.1).to(dev)
+    x = torch.randn(1, M, D, device=dev, generator=g).to(torch.bfloat16)
+    xin = torch.randn(1, M, D, device=dev, generator=g).to(torch.bfloat16)
+    h = torch.empty(1, M, 9, I, dtype=torch.bfloat16, device=dev)
+    probs = torch.empty(1, M, 8, device=dev)
+    idx = torch.empty(1, M, 8, dtype=torch.int32, device=dev)
+    y = torch.empty(1, M, D, dtype=torch.bfloat16, device=dev)
+
+    def moe_step(i):
+        up, dn = copies[i % 2]
+        expert_select_up_gate_silu(x, scores[i], bias, up, h, probs, idx, None, model_arch="deepseek_v3_2")
+        expert_down_allreduce(h, dn, None, idx, probs, xin, 0, y)
+    us = _graph_time_us(torch, moe_step, st, 5)
+    hits = []
+    for sc in scores:
+        pr = torch.empty(1, M, 8, device=dev)
+        ix = torch.empty(1, M, 8, dtype=torch.int32, device=dev)
+        from tilert_amd.expert_sel_up_gate_silu import expert_select
+        expert_select(sc, bias, pr, ix, model_arch="deepseek_v3_2")
+        hits.append(1 + len(set(ix.flatten().tolist())))
+    mh = sum(hits) / len(hits)
+    b = mh * (3 * I * D + 3 * (I // 128) * (D // 128) * 4) + M * D * 2 * 3 + M * 9 * I * 2 * 2
+    out["moe_ref_layout_M4"] = {"us": round(us, 2), "mean_hit_experts": round(mh, 2), "bytes_per_call": round(b),
+                                "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del copies
+    torch.cuda.empty_cache()
+
+    # dense MLP share: 9 chunks x 256 rows, four weight copies rotated
+    dense = [(UpGateExperts(*stack(I, D, 9), *stack(I, D, 9)), DownExperts(*stack(D, I, 9))) for _ in range(8)]
+    gam = torch.rand(D, device=dev, generator=g) + 0.5
+    hd = torch.empty(1, M, 9, I, dtype=torch.bfloat16, device=dev)
+
+    def dense_step(i):
+        up, dn = dense[i % 8]
+        rmsnorm_up_gate_silu(x, gam, up, hd, None, "deepseek_v3_2")
+        down_allreduce(hd, dn, None, xin, 0, y, None, "deepseek_v3_2")
+    us = _graph_time_us(torch, dense_step, st, 5)
+    b = 9 * 3 * I * D + M * D * 2 * 3 + M * 9 * I * 2 * 2
+    out["dense_mlp_share_M4"] = {"us": round(us, 2), "bytes_per_call": b, "GBs": round(b / us / 1e3, 1),
+                                 "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del dense
+
+    # absorbed MLA projections at the 16-head share
+    H = 16
+    wkv = [K_.weight_quant(torch.randn(H * 256, 512, device=dev, generator=g) * 0.02) for _ in range(8)]
+    pq = [convert_projq_wqb(q, s_, H) for q, s_ in wkv]
+    po = [convert_projo_wkvb(q, s_, H) for q, s_ in wkv]
+    wo = [convert_unproj_o(*K_.weight_quant(torch.randn(D, H * 128, device=dev, generator=g) * 0.02)) for _ in range(4)]
+    qn = torch.randn(1, M, H, 128, device=dev, generator=g).to(torch.bfloat16)
+    ol = torch.randn(1, M, H, 512, device=dev, generator=g).to(torch.bfloat16)
+    ql = torch.empty(1, M, H, 512, dtype=torch.bfloat16, device=dev)
+    ov = torch.empty(1, M, H, 128, dtype=torch.bfloat16, device=dev)
+    res = {}
+    us = _graph_time_us(torch, lambda i: projq_wqb(qn, pq[i % 8], None, ql, None, model_arch="deepseek_v3_2"), st, 5)
+    res["projq_wqb"] = {"us": round(us, 2), "GBs": round((H * 128 * 512) / us / 1e3, 1)}
+    us = _graph_time_us(torch, lambda i: projo_wkvb(ol, po[i % 8], None, ov, None, "deepseek_v3_2"), st, 5)
+    res["projo_wkvb"] = {"us": round(us, 2), "GBs": round((H * 128 * 512) / us / 1e3, 1)}
+    us = _graph_time_us(torch, lambda i: unproj_o_allreduce(ov, wo[i % 4], None, xin, 0, y, None, "deepseek_v3_2"),
+                        st, 5)
+    res["unproj_o_allreduce"] = {"us": round(us, 2), "GBs": round((D * H * 128) / us / 1e3, 1)}
+    out["mla_absorbed_M4"] = res
+    return out
+
 
 # ----------------------------------------------------------------------------- extras
 def _cpu_time_us(torch, fn, reps=3):
@@ -414,6 +505,8 @@ def extras(torch, steps, dev):
             sweep[f"{tag}_M{M}"] = e
         del ws
     out["m_sweep"] = sweep
+
+    out.update(bench_ref_layout(torch, steps, dev))
 
     # configs 2 and 4 are part of the default line; here the paged form of config 4
     M, H, L = 4, 64, 131072
