@@ -49,6 +49,8 @@ def _run(M, E, D, I, topk, n_experts, e0, seed, idx=None, w=None):
     (3, 32, 7168, 2048, 8, 256, 32),  # config 2 shapes (shard 1 of 8), odd M
     (4, 32, 7168, 2048, 8, 256, 32),  # config 2: M = 4, shard 1 of 8
     (4, 32, 7168, 2048, 8, 256, 224),  # config 2: M = 4, shard 7 of 8
+    (4, 32, 7168, 2048, 8, 32, 0),  # every expert local: ~20 hits, several down batches,
+                                    # more gate/up items than gate/up workgroups
     (16, 8, 512, 256, 8, 32, 0),  # 128 routed pairs: the kernels without LDS activations
     (8, 4, 7168, 256, 2, 16, 0),  # x [8, 7168] exceeds 64 KB: gate/up without LDS, down with
 ])
