@@ -188,7 +188,14 @@ def bench_moe(torch, steps, dev, cpu=True):
     b = mean_hits * per_expert + M * D * 2 * 2 + mean_hits * M * I * 2 * 2
     res = {"us": round(us, 2), "mean_hit_experts": round(mean_hits, 3), "bytes_per_call": round(b),
            "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-           "routings": len(routes), "weight_copies_rotated": 2}
+           "routings": len(routes), "weight_copies_rotated": 2,
+           "roofline": {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic("moe_ep8_M4.md"),
+                        "traffic_source": "profiles/moe_ep8_M4.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                                          "gate/up + down per call, same routings)",
+                        "kernel": "tl::moe_gate_up_lds_kernel + tl::moe_down_lds_kernel<2>",
+                        "bytes_per_call": round(b)}}
     del copies
     if cpu:
         # the reference torch path on the host cores over the SAME routings the GPU ran (a
@@ -218,7 +225,8 @@ def bench_moe(torch, steps, dev, cpu=True):
             moe_cpu(idx, w)
         cus = (time.perf_counter_ns() - t0) / 1e3 / len(sample)
         s_hits = sum(hits[:len(sample)]) / len(sample)
-        res["cpu_baseline"] = {"us": round(cus, 1), "cores": len(os.sched_getaffinity(0)), "kind": "port",
+        res["cpu_baseline"] = {"value": round(b / cus / 1e3, 2), "unit": "GB/s", "us": round(cus, 1),
+                               "cores": len(os.sched_getaffinity(0)), "kind": "port",
                                "sample": f"the first {len(sample)} of the GPU's {len(routes)} routings "
                                          f"({s_hits:.2f} mean hit experts), one call each after a warm-up"}
         del deq
@@ -264,7 +272,13 @@ def bench_indexer(torch, steps, dev, cpu=True, keep=False):
            "bytes_per_call": b_all, "GBs": round(b_all / us_b / 1e3, 1),
            "hbm_frac": round(b_all / us_b / 1e3 / HBM_PEAK_GBS, 4),
            "scores_hbm_frac": round(b_s / us_s / 1e3 / HBM_PEAK_GBS, 4),
-           "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 4), "caches_rotated": 20}
+           "scores_mfma_util": round(flops / us_s / 1e6 / FP8_PEAK_TFLOPS, 4), "caches_rotated": 20,
+           "roofline": {"bound": "hbm", "achieved": round(b_all / us_b / 1e3, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(b_all / us_b / 1e3 / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic("indexer_topk_128k_M4.md"),
+                        "traffic_source": "profiles/indexer_topk_128k_M4.md (rocprofv3 --pmc FETCH_SIZE, "
+                                          "WRITE_SIZE; indexer + top-k per call)",
+                        "kernel": "tl::indexer_kernel + tl::topk_kernel", "bytes_per_call": b_all}}
     if cpu:
         # the reference torch path on the host cores: fp32 einsum of the dequantised q and
         # keys, ReLU, head-weighted sum, causal mask, torch.topk (ops/topk.py:128-143)
@@ -278,7 +292,9 @@ def bench_indexer(torch, steps, dev, cpu=True, keep=False):
             lim = (L - 4 + torch.arange(M))[:, None]
             lg = torch.where(torch.arange(L)[None, :] <= lim, lg, torch.tensor(float("-inf")))
             return lg.topk(k, dim=-1).indices
-        res["cpu_baseline"] = {"us": _cpu_time_us(torch, idx_cpu), "cores": len(os.sched_getaffinity(0)),
+        cus = _cpu_time_us(torch, idx_cpu)
+        res["cpu_baseline"] = {"value": round(b_all / cus / 1e3, 3), "unit": "GB/s", "us": cus,
+                               "cores": len(os.sched_getaffinity(0)),
                                "kind": "port", "sample": "the full workload on one of the 20 caches, median of 3 "
                                                          "after a warm-up"}
         del qd_c, kd_c
@@ -287,6 +303,7 @@ def bench_indexer(torch, steps, dev, cpu=True, keep=False):
     del caches
     torch.cuda.empty_cache()
     return res
+
 
 def bench_ref_layout(torch, steps, dev):
     """The reference's own operator layouts at one device's share (DeepSeek-V3.2, M = 4):
