@@ -204,7 +204,7 @@ def bench_moe(torch, steps, dev, cpu=True):
         # 455-468), the bf16 weights of every hit expert dequantised beforehand (as
         # init_reference_weights does) and widened per use, as the goldens do
         from oracle import reference as ref  # the checker/baseline only
-        sample = routes[:min(len(routes), 8)]
+        sample = routes  # every routing the GPU ran
         need = sorted({e for i, _ in sample for e in ref.hit_experts(i, e0, E)})
         deq = {e: [ref.weight_dequant(parts0[2 * j][e].cpu(), parts0[2 * j + 1][e].cpu()).to(torch.bfloat16)
                    for j in range(3)] for e in need}
