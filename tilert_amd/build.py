@@ -33,9 +33,16 @@ FLAGS = [
 ]
 
 
+# Per-source extra flags.  indexer: MFMA results in VGPRs (its epilogue reads every result
+# with VALU ops; in AGPRs each element would first need a v_accvgpr_read).
+EXTRA = {
+    "indexer": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src.stem, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")

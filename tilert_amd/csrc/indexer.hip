@@ -4,14 +4,12 @@
 // every scale is positive (the form of sparse_index_op, ops/sparse_index.py:11-69, on the
 // fp8 cache layout of pd_vllm/profiles/mla_nsa.py:211-228).
 //
-// gfx950 mapping: the M*H query rows form M*H/16 tiles of 16 rows x 128 dims, staged
-// once per workgroup through LDS (in MFMA fragment order); each wave holds the tiles of
-// its tokens in registers (A operand) and takes its own range of 16-key tiles (B operand,
-// 2 KB contiguous each) through the native fp8 MFMA v_mfma_f32_16x16x128_f8f6f4 -- one
-// MFMA is a whole 128-long dot product for 16 heads x 16 keys.  Epilogue per MFMA: ReLU
-// (one integer max) and the head weight (one FMA); the head sum over a lane's 4 heads
-// and a token's tiles stays in registers, and the 4 lane groups are combined with
-// v_permlane32_swap / v_permlane16_swap.
+// gfx950 mapping: the M*H query rows form M*H/16 tiles of 16 rows x 128 dims; a wave holds
+// 4 of them in registers (A operands: one token at H = 64, two at H = 32) and scores 16-key
+// tiles (B operands, 2 KB contiguous each) through the native fp8 MFMA
+// v_mfma_f32_16x16x128_f8f6f4 -- one MFMA is a whole 128-long dot product for 16 heads x
+// 16 keys.  Epilogue per MFMA: ReLU (one integer max) and the head weight (one FMA) into a
+// per-lane partial over the lane's 4 heads of each query tile.
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
@@ -21,48 +19,13 @@ namespace tl {
 // fmaxf(x, 0) costs two instructions under IEEE mode (a NaN-quieting max first).
 __device__ inline float relu(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 
-constexpr int kIdxWaves = 8;  // waves per workgroup
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr int kBufWord3 = 0x00020000;     // buffer resource word 3: 32-bit data format
+constexpr int kBufNonTemporal = 2;        // buffer access cache policy: nt (streamed once)
 
-// Work split.  A wave scores TW tokens (at most 4 query tiles, held in registers) against
-// TPW key tiles; the SPLIT = ceil(M / TW) waves that share a key range sit in the same
-// workgroup, KW = 8 / SPLIT ranges per workgroup, KW * TPW contiguous key tiles in all.
-//
-// Key path: the key cache is row-major [L, 128], but the MFMA wants lane (r, g) to hold
-// 32 bytes of key r -- a strided read (16 rows per instruction) that measured ~2 us
-// slower over 16 MB than contiguous 1 KB reads.  So the workgroup reads its key tiles
-// contiguously into LDS (16-byte chunk c of row r stored at chunk position c ^ (r & 7):
-// the MFMA-layout reads are then free of bank conflicts), in PH phases that are all
-// requested at kernel start; phase p is computed while the later phases still arrive.
-// Query tiles (in MFMA fragment order), folded head weights and key scales are staged
-// in LDS by the same loads.  Every loop is unrolled with compile-time trip counts, all
-// loads are unconditional (indices clamped), and scores stay in registers until the
-// end, so no wait covers a later load or a store.
-template <int M, int H, int TW, int TPW>
-struct IdxShape {
-  static constexpr int TPT = H / 16;              // query tiles per token
-  static constexpr int QT = M * TPT;              // query tiles
-  static constexpr int QTW = TW * TPT;            // query tiles per wave
-  static constexpr int SPLIT = (M + TW - 1) / TW; // waves per key range
-  static constexpr int KW = kIdxWaves / SPLIT;    // key ranges per workgroup
-  static constexpr int PH = TPW >= 2 ? 2 : 1;     // key phases
-  static constexpr int TPP = TPW / PH;            // tiles per range per phase
-  static constexpr int PT = KW * TPP;             // tiles per phase (workgroup)
-  static constexpr int NT = KW * TPW;             // key tiles per workgroup
-  static constexpr int THREADS = kIdxWaves * 64;
-  static constexpr int QCH = QT * 128;            // 16-byte query chunks
-  static constexpr int QPT = (QCH + THREADS - 1) / THREADS;
-  static constexpr int KPT = (PT * 128 + THREADS - 1) / THREADS;  // key chunks per thread per phase
-  static constexpr int KSPT = (NT * 16 + THREADS - 1) / THREADS;  // key scales per thread
-  // LDS carve-up (bytes)
-  static constexpr int Q_OFF = 0;
-  static constexpr int WQ_OFF = Q_OFF + QPT * THREADS * 16;
-  static constexpr int KS_OFF = WQ_OFF + THREADS * 4;
-  static constexpr int K_OFF = KS_OFF + KSPT * THREADS * 4;
-  static constexpr int K_BYTES = KPT * THREADS * 16;  // one phase buffer
-  static constexpr int LDS = K_OFF + PH * K_BYTES;
-  static_assert(kIdxWaves % SPLIT == 0 && TW <= 4 && QT * 16 <= THREADS, "work split");
-};
+// A buffer's record count from a byte count (an int64 ternary, so it stays scalar: HIP's
+// int64 min() goes through f64 VALU ops, which makes the resource divergent).
+__device__ inline int clamp_records(int64_t bytes) { return bytes < 0x7fffffff ? static_cast<int>(bytes) : 0x7fffffff; }
 
 // Key cache layouts.  Flat: fp8 [L, 128] plus fp32 scales [L].  Paged (PAGED): the
 // 64-token pages of pd_vllm/profiles/mla_nsa.py:38-41,211-228 -- page p is 64 x 128 fp8
@@ -71,152 +34,190 @@ struct IdxShape {
 constexpr int kKiPageKeys = 64;
 constexpr int kKiPageBytes = kKiPageKeys * 128 + kKiPageKeys * 4;  // 8448
 
-template <bool PAGED>
-__device__ inline int64_t key_tile_byte(int tile) {
-  return PAGED ? static_cast<int64_t>(tile >> 2) * kKiPageBytes + (tile & 3) * 2048 : static_cast<int64_t>(tile) * 2048;
-}
 
-template <int M, int H, int TW, int TPW, bool PAGED>
-__global__ __launch_bounds__(kIdxWaves * 64) void indexer_kernel(
+// Work split.  A workgroup owns KW key ranges of NTR contiguous key tiles; SPLIT waves
+// share each range (wave sp of a range holds query tiles 4 sp .. 4 sp + 3), so the
+// range's key tiles go through LDS once for all of them.  All global loads are requested
+// at kernel start -- queries, head weights and key scales straight into registers in the
+// layouts they are used in (one coalesced load per lane for the weights and scales, spread
+// by lane shuffles), then the key tiles quad by quad (4 tiles = 64 keys) as contiguous
+// 1 KB reads -- and quad s is put into LDS and scored as soon as it has landed while the
+// later quads still arrive; quad s + 1's MFMAs are issued before quad s's epilogue.  The
+// head sum over the 4 lane groups is done for a whole quad at once: two v_permlane32_swap
+// and one v_permlane16_swap leave lane l with the total of key 16 (l / 16) + l % 16 of
+// the quad (3 swaps and 3 adds per quad instead of 2 + 2 per tile), so each lane scales,
+// masks and stores one score: one 256-byte contiguous store per wave, token and quad.
+template <int M, int H, int NTR>
+struct IdxShape {
+  static constexpr int TPT = H / 16;                   // query tiles per token
+  static constexpr int QT = M * TPT;                   // query tiles
+  static constexpr int TW = 4 / TPT;                   // tokens per wave (4 tile slots)
+  static constexpr int SPLIT = (QT + 3) / 4;           // waves per key range
+  static constexpr int KW = SPLIT >= 4 ? 1 : 4 / SPLIT;  // key ranges per workgroup
+  static constexpr int WAVES = SPLIT * KW;
+  static constexpr int THREADS = WAVES * 64;
+  static constexpr int NQ = NTR / 4;                   // quads per range
+  static constexpr int NT = KW * NTR;                  // key tiles per workgroup
+  static constexpr int QCH = KW * 4 * 128;             // 16-byte key chunks per quad step
+  static constexpr int CPT = (QCH + THREADS - 1) / THREADS;
+  static constexpr int LDS = NT * 2048 + 2048;         // + a dump row for padding chunks
+  static_assert(NTR % 4 == 0 && TPT * TW == 4, "shape");
+};
+
+template <int M, int H, int NTR, bool PAGED>
+__global__ __launch_bounds__(256) void indexer_kernel(
     const uint8_t* __restrict__ q, const float* __restrict__ q_s, int q_s_per_head,
     const uint8_t* __restrict__ k, const float* __restrict__ k_s, const uint16_t* __restrict__ w,
     float* __restrict__ logits, int L, int64_t ld, int64_t cur_pos, int n_tiles) {
-  using S = IdxShape<M, H, TW, TPW>;
+  using S = IdxShape<M, H, NTR>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int t0 = (wave % S::SPLIT) * TW;  // first token of this wave
-  const int rr = wave / S::SPLIT;         // key range of this wave
-  const int wg_tile = blockIdx.x * S::NT; // first key tile of the workgroup
+  const int sp = wave % S::SPLIT;          // which 4 query tiles
+  const int rr = wave / S::SPLIT;          // which key range
+  const int wg_tile = blockIdx.x * S::NT;  // first key tile of the workgroup
+  const int r_tile = wg_tile + rr * NTR;   // first key tile of this wave's range
 
-  // ---- all global loads, issued together
-  // query chunk d of the LDS image (fragment order): tile d / 128, piece (d / 64) % 2,
-  // lane d % 64 -> row 16 qt + l % 16, 16-byte piece 4 p + l / 16 of that row
-  uint4 qv[S::QPT];
+  // ---- every load is a buffer load from a workgroup-uniform base with a 32-bit lane
+  //      offset; records past the end read as zero, so no lane clamps its address.
+  //      All are unconditional and issued before any result is used, so the only waits
+  //      are the compiler's in-order counts for the operands of each step.
+  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(q), 0, S::QT * 2048, kBufWord3);
+  v8i qa[4];
 #pragma unroll
-  for (int u = 0; u < S::QPT; ++u) {
-    const int d = min(tid + u * S::THREADS, S::QCH - 1);
-    const int qt = d >> 7, pp = (d >> 6) & 1, l = d & 63;
-    qv[u] = reinterpret_cast<const uint4*>(q)[((qt * 16 + (l & 15)) << 3) + pp * 4 + (l >> 4)];
-  }
-  const int wrow = min(tid, S::QT * 16 - 1);
-  const float wqv = bf16_to_f32(w[wrow]) * q_s[q_s_per_head ? wrow : wrow / H];
-  float ksv[S::KSPT];
-#pragma unroll
-  for (int u = 0; u < S::KSPT; ++u) {
-    const int e = tid + u * S::THREADS;  // key e % 16 of workgroup tile e / 16
-    const int key = min(min(wg_tile + e / 16, n_tiles - 1) * 16 + (e & 15), L - 1);
-    ksv[u] = PAGED ? *reinterpret_cast<const float*>(k + static_cast<int64_t>(key / kKiPageKeys) * kKiPageBytes +
-                                                     kKiPageKeys * 128 + (key % kKiPageKeys) * 4)
-                   : k_s[key];
-  }
-  // key chunk c of phase p: phase tile pt = c / 128 (range pt / TPP, its tile
-  // p * TPP + pt % TPP), row (c / 8) % 16, 16-byte chunk c % 8 -- contiguous 1 KB reads
-  auto key_src = [&](int p, int c) {
-    const int pt = min(c >> 7, S::PT - 1);
-    const int tile = min(wg_tile + (pt / S::TPP) * TPW + p * S::TPP + pt % S::TPP, n_tiles - 1);
-    const int64_t byte = key_tile_byte<PAGED>(tile) + (c & 127) * 16;
-    // flat: a short last tile stops at the cache end; paged: pages are whole
-    return reinterpret_cast<const u32x4v*>(k + (PAGED ? byte : min(byte, static_cast<int64_t>(L) * kBlock - 16)));
-  };
-  u32x4v kv[S::PH][S::KPT];
-#pragma unroll
-  for (int p = 0; p < S::PH; ++p)
-#pragma unroll
-    for (int u = 0; u < S::KPT; ++u) kv[p][u] = __builtin_nontemporal_load(key_src(p, tid + u * S::THREADS));
-
-  // ---- stage queries, weights, key scales and key phase 0
-  uint4* q_lds = reinterpret_cast<uint4*>(smem + S::Q_OFF);
-  float* wq_lds = reinterpret_cast<float*>(smem + S::WQ_OFF);
-  float* ks_lds = reinterpret_cast<float*>(smem + S::KS_OFF);
-  auto key_lds = [&](int p) { return smem + S::K_OFF + p * S::K_BYTES; };
-  auto put_keys = [&](int p) {
-#pragma unroll
-    for (int u = 0; u < S::KPT; ++u) {
-      const int c = tid + u * S::THREADS;  // chunks past the phase land in the padding
-      const int row = (c >> 3) & 15, ch = c & 7;
-      *reinterpret_cast<u32x4v*>(key_lds(p) + (c >> 7) * 2048 + row * 128 + ((ch ^ (row & 7)) << 4)) = kv[p][u];
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < S::QPT; ++u) q_lds[tid + u * S::THREADS] = qv[u];
-  wq_lds[tid] = wqv;
-#pragma unroll
-  for (int u = 0; u < S::KSPT; ++u) ks_lds[tid + u * S::THREADS] = ksv[u];
-  put_keys(0);
-  __syncthreads();
-
-  // ---- this wave's query tiles (A operands) and head weights; tokens past M (a short
-  //      last group) repeat token M-1 and are not stored
-  v8i qa[S::QTW];
-  float4 wq[S::QTW];
-#pragma unroll
-  for (int j = 0; j < S::QTW; ++j) {
-    const int qt = min(t0 + j / S::TPT, M - 1) * S::TPT + j % S::TPT;
-    const uint4 lo = q_lds[qt * 128 + lane];
-    const uint4 hi = q_lds[qt * 128 + 64 + lane];
+  for (int j = 0; j < 4; ++j) {
+    const int qt = min(4 * sp + j, S::QT - 1);
+    const int qo = (qt * 16 + r) * 128 + g * 16;
+    const u32x4v lo = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo, 0, 0);
+    const u32x4v hi = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo + 64, 0, 0);
     qa[j] = v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
                 static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
-    wq[j] = *reinterpret_cast<const float4*>(wq_lds + qt * 16 + 4 * g);
   }
-
-  float out[TPW];  // lane group g < TW: token t0 + g of key r
+  // head weights and query scales of the wave's 64 (token, head) rows: one load each per
+  // lane (lane l holds row 64 sp + l), spread to the MFMA layout by lane shuffles later
+  const int hrow = min(64 * sp + lane, S::QT * 16 - 1);
+  const uint16_t wraw = w[hrow];
+  const float qsraw = q_s[q_s_per_head ? hrow : hrow / H];
+  // key bytes of this workgroup: flat from tile wg_tile, paged from page wg_tile / 4
+  // (NTR % 4 == 0, so a workgroup starts on a page); a quad of 4 tiles is one page
+  const int64_t kbase = PAGED ? static_cast<int64_t>(wg_tile / 4) * kKiPageBytes : static_cast<int64_t>(wg_tile) * 2048;
+  const int64_t kend = PAGED ? cdiv(n_tiles, 4) * kKiPageBytes : static_cast<int64_t>(L) * kBlock;
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(k) + kbase, 0, clamp_records(kend - kbase), kBufWord3);
+  const __amdgpu_buffer_rsrc_t srs = PAGED ? krs
+      : __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(k_s) + wg_tile * 16, 0,
+                                          clamp_records((static_cast<int64_t>(L) - wg_tile * 16) * 4), kBufWord3);
+  auto tile_off = [](int lt) { return PAGED ? (lt >> 2) * kKiPageBytes + (lt & 3) * 2048 : lt * 2048; };
+  float ksv[S::NQ];  // key r_tile * 16 + 64 s + lane
 #pragma unroll
-  for (int p = 0; p < S::PH; ++p) {
-    if (p > 0) {  // the next phase's keys have (mostly) arrived while this one computed
-      put_keys(p);
-      __syncthreads();
+  for (int s = 0; s < S::NQ; ++s) {
+    const int lt = rr * NTR + 4 * s;  // workgroup-local first tile of the quad
+    ksv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+        srs, PAGED ? (lt >> 2) * kKiPageBytes + kKiPageKeys * 128 + lane * 4 : (lt * 16 + lane) * 4, 0, 0));
+  }
+  // ---- key quads: chunk c of step s -> range c / 512, tile 4 s + (c / 128) % 4, row
+  //      (c / 8) % 16, 16-byte piece c % 8 (contiguous 1 KB reads)
+  u32x4v kv[S::NQ][S::CPT];
+#pragma unroll
+  for (int s = 0; s < S::NQ; ++s)
+#pragma unroll
+    for (int u = 0; u < S::CPT; ++u) {
+      const int c = min(tid + u * S::THREADS, S::QCH - 1);
+      const int lt = (c >> 9) * NTR + 4 * s + ((c >> 7) & 3);
+      kv[s][u] = __builtin_amdgcn_raw_buffer_load_b128(krs, tile_off(lt) + (c & 127) * 16, 0, kBufNonTemporal);
     }
+  // scheduling boundary: nothing below (which waits for loads) moves above the requests
+  asm volatile("" ::: "memory");
+  // lane (r, g) needs heads 4 g .. 4 g + 3 of each of its 4 query tiles: rows 16 j + 4 g + e
+  const float wqv = bf16_to_f32(wraw) * qsraw;
+  float4 wq[4];
 #pragma unroll
-    for (int ii = 0; ii < S::TPP; ++ii) {
-      const int i = p * S::TPP + ii;
-      const uint8_t* tile = key_lds(p) + (rr * S::TPP + ii) * 2048 + r * 128;
+  for (int j = 0; j < 4; ++j)
+    wq[j] = make_float4(__shfl(wqv, 16 * j + 4 * g), __shfl(wqv, 16 * j + 4 * g + 1), __shfl(wqv, 16 * j + 4 * g + 2),
+                        __shfl(wqv, 16 * j + 4 * g + 3));
+#pragma unroll
+  for (int s = 0; s < S::NQ; ++s) asm volatile("" : "+v"(ksv[s]));  // keep the scale loads up front
+
+  const int tok0 = (4 * sp) / S::TPT;  // first token of this wave
+  // put quad s into LDS (piece c of row r stored at piece c ^ (r & 7): conflict-free
+  // MFMA-layout reads)
+  auto put = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < S::CPT; ++u) {
+      const int c = tid + u * S::THREADS;
+      const int row = (c >> 3) & 15, ch = c & 7;
+      const int lt = (c >> 9) * NTR + 4 * s + ((c >> 7) & 3);  // workgroup-local tile
+      uint8_t* dst = c < S::QCH ? smem + lt * 2048 + row * 128 + ((ch ^ (row & 7)) << 4) : smem + S::NT * 2048;
+      *reinterpret_cast<u32x4v*>(dst) = kv[s][u];
+    }
+  };
+  auto products = [&](int s, v4f (&c)[4][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint8_t* tile = smem + (rr * NTR + 4 * s + i) * 2048 + r * 128;
       const uint4 lo = *reinterpret_cast<const uint4*>(tile + ((g ^ (r & 7)) << 4));
       const uint4 hi = *reinterpret_cast<const uint4*>(tile + (((g + 4) ^ (r & 7)) << 4));
       const v8i kt = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
                       static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
-      // all MFMAs of the tile first, into separate results, then the epilogue
-      v4f c[S::QTW];
 #pragma unroll
-      for (int j = 0; j < S::QTW; ++j) c[j] = mfma_16x16x128_fp8(qa[j], kt);
-      const float ksc = ks_lds[(rr * TPW + i) * 16 + r];
-      float score[TW];
+      for (int j = 0; j < 4; ++j) c[i][j] = mfma_16x16x128_fp8(qa[j], kt);
+    }
+  };
+  auto epilogue = [&](int s, const v4f (&c)[4][4]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < TW; ++t) {
+    for (int t = 0; t < S::TW; ++t) {
+      // lane partial (its 4 heads of each of the token's query tiles) per tile of the quad
+      float a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
         float acc = 0.f;
 #pragma unroll
         for (int jj = 0; jj < S::TPT; ++jj) {
           const int j = t * S::TPT + jj;
-          acc = __builtin_fmaf(relu(c[j][0]), wq[j].x, acc);
-          acc = __builtin_fmaf(relu(c[j][1]), wq[j].y, acc);
-          acc = __builtin_fmaf(relu(c[j][2]), wq[j].z, acc);
-          acc = __builtin_fmaf(relu(c[j][3]), wq[j].w, acc);
+          acc = __builtin_fmaf(relu(c[i][j][0]), wq[j].x, acc);
+          acc = __builtin_fmaf(relu(c[i][j][1]), wq[j].y, acc);
+          acc = __builtin_fmaf(relu(c[i][j][2]), wq[j].z, acc);
+          acc = __builtin_fmaf(relu(c[i][j][3]), wq[j].w, acc);
         }
-        // lanes r, r+16, r+32, r+48 hold the 4 partial head sums of key r: sum them with
-        // the gfx950 lane-swap instructions (VALU, no LDS round trip)
-        const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc), __float_as_uint(acc), false, false);
-        const float y = __uint_as_float(s32[0]) + __uint_as_float(s32[1]);
-        const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false, false);
-        score[t] = (__uint_as_float(s16[0]) + __uint_as_float(s16[1])) * ksc;
+        a[i] = acc;
       }
-      float v = score[0];
-#pragma unroll
-      for (int tt = 1; tt < TW; ++tt)
-        if (tt == g) v = score[tt];
-      out[i] = v;
+      // rows (16-lane groups) hold partial sums over disjoint heads: pair tiles (0, 2)
+      // and (1, 3) across the 32-lane halves, then the two results across odd/even rows;
+      // lane group g ends with the total of tile g
+      const auto p02 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[2]), false, false);
+      const auto p13 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[1]), __float_as_uint(a[3]), false, false);
+      const float x = __uint_as_float(p02[0]) + __uint_as_float(p02[1]);
+      const float y = __uint_as_float(p13[0]) + __uint_as_float(p13[1]);
+      const auto pxy = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+      const float score = (__uint_as_float(pxy[0]) + __uint_as_float(pxy[1])) * ksv[s];
+      const int tok = tok0 + t;  // wave-uniform
+      if (tok < M) {
+        // keys past L are dropped by the buffer's bound; keys past the token's position
+        // (cur_pos + tok, at most L - 1 here) are masked
+        const int key = (r_tile + 4 * s) * 16 + lane;
+        const int lim = cur_pos + tok < L ? static_cast<int>(cur_pos + tok) : L - 1;
+        const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(logits + tok * ld, 0, L * 4, kBufWord3);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, key > lim ? -__builtin_inff() : score), ors,
+                                              key * 4, 0, 0);
+      }
     }
-  }
-
-  // lane group g stores token t0 + g: a 64-byte row segment per tile
-  const int tok = t0 + g;
-  const int t_begin = wg_tile + rr * TPW;
+  };
+  // software pipeline: quad s + 1's MFMAs are issued before quad s's epilogue, so the
+  // matrix core works while the VALU finishes the previous quad
+  v4f cb[2][4][4];
+  put(0);
+  __syncthreads();
+  products(0, cb[0]);
 #pragma unroll
-  for (int i = 0; i < TPW; ++i) {
-    const int key = (t_begin + i) * 16 + r;
-    if (g < TW && tok < M && t_begin + i < n_tiles && key < L)
-      logits[static_cast<int64_t>(tok) * ld + key] = static_cast<int64_t>(key) > cur_pos + tok ? -__builtin_inff() : out[i];
+  for (int s = 0; s < S::NQ; ++s) {
+    if (s + 1 < S::NQ) {
+      put(s + 1);
+      __syncthreads();
+      products(s + 1, cb[(s + 1) & 1]);
+    }
+    epilogue(s, cb[s & 1]);
   }
 }
 
@@ -229,48 +230,37 @@ __global__ void fill_masked_kernel(float* __restrict__ logits, int M, int64_t ld
   logits[t * ld + c] = -__builtin_inff();
 }
 
-constexpr int kIdxMaxWaves = 4096;  // 16 per CU: beyond that a wave takes more key tiles
 
-template <int M, int H, int TW, int TPW, bool PAGED>
-static int launch_indexer_t(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
-                            const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
-                            int L, int64_t ld, int64_t cur_pos, int n_tiles) {
-  using S = IdxShape<M, H, TW, TPW>;
-  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, TW, TPW, PAGED>);
+template <int M, int H, int NTR, bool PAGED>
+static int launch_indexer_t(hipStream_t st, const uint8_t* q, const float* q_s, int per_head, const uint8_t* k,
+                            const float* k_s, const uint16_t* w, float* logits, int L, int64_t ld, int64_t cur_pos,
+                            int n_tiles) {
+  using S = IdxShape<M, H, NTR>;
+  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, NTR, PAGED>);
   if (S::LDS > 64 * 1024) {
     const int rc = allow_dynamic_lds(fn, S::LDS, "indexer");
     if (rc) return rc;
   }
   const dim3 grid(static_cast<unsigned>(cdiv(n_tiles, static_cast<int64_t>(S::NT))));
-  hipLaunchKernelGGL((indexer_kernel<M, H, TW, TPW, PAGED>), grid, dim3(kIdxWaves * 64), S::LDS, st, q, q_s, per_head, k,
-                     k_s, w, logits, L, ld, cur_pos, n_tiles);
+  hipLaunchKernelGGL((indexer_kernel<M, H, NTR, PAGED>), grid, dim3(S::THREADS), S::LDS, st, q, q_s, per_head, k, k_s,
+                     w, logits, L, ld, cur_pos, n_tiles);
   return check_launch("indexer");
 }
 
-// Tokens per wave: at most 4 query tiles (one token at H = 64), so a wave stays near 100
-// VGPRs and 4 waves share each SIMD (measured 5% faster than 8 query tiles at 2 waves per
-// SIMD); raised where needed so that the waves sharing a key range divide the workgroup.
-constexpr int pick_tw(int M, int TPT) {
-  int tw = (4 / TPT < M) ? 4 / TPT : M;
-  while (tw < M && (kIdxWaves % ((M + tw - 1) / tw) != 0)) ++tw;
-  return tw;
-}
-
+// Key tiles per range: 16 (4 quads; two 4-wave workgroups per CU at M = 4, H = 64 --
+// measured against 8 and 32 at 128K keys: 8.0 vs 8.4 / 8.4 us) while that still gives
+// >= 512 workgroups, fewer for short caches so the grid keeps filling the chip.
 template <int M, int H, bool PAGED>
 static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
                           const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
                           int L, int64_t ld, int64_t cur_pos, int n_tiles) {
-  constexpr int TPT = H / 16;
-  constexpr int TW = pick_tw(M, TPT);
-  constexpr int SPLIT = (M + TW - 1) / TW;
-  // smallest tiles-per-wave that keeps the grid within 8 waves per CU
-  int tpw = 1;
-  while (tpw < 8 && static_cast<int64_t>(n_tiles) * SPLIT > static_cast<int64_t>(kIdxMaxWaves) * tpw) tpw *= 2;
-  switch (tpw) {
-    case 1: return launch_indexer_t<M, H, TW, 1, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    case 2: return launch_indexer_t<M, H, TW, 2, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    case 4: return launch_indexer_t<M, H, TW, 4, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    default: return launch_indexer_t<M, H, TW, 8, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+  constexpr int KW = IdxShape<M, H, 4>::KW;
+  int ntr = 16;
+  while (ntr > 4 && cdiv(n_tiles, static_cast<int64_t>(KW) * ntr) < 512) ntr /= 2;
+  switch (ntr) {
+    case 4: return launch_indexer_t<M, H, 4, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    case 8: return launch_indexer_t<M, H, 8, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+    default: return launch_indexer_t<M, H, 16, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
   }
 }
 
@@ -280,7 +270,7 @@ static int indexer_scores(const char* who, const void* q_fp8, const float* q_s, 
                           int64_t ld, int64_t cur_pos, void* stream) {
   if (H != 32 && H != 64) { set_error("%s: H=%lld must be 32 or 64", who, (long long)H); return kErrUnsupported; }
   if (M < 1 || M * H > 256) { set_error("%s: need 1 <= M and M*H <= 256 (M=%lld H=%lld)", who, (long long)M, (long long)H); return kErrUnsupported; }
-  if (L < 0 || L > (1ll << 30) || ld < L) { set_error("%s: bad L=%lld / ld=%lld", who, (long long)L, (long long)ld); return kErrArg; }
+  if (L < 0 || L > (1ll << 28) || ld < L) { set_error("%s: bad L=%lld / ld=%lld", who, (long long)L, (long long)ld); return kErrArg; }
   if (cur_pos < 0) { set_error("%s: cur_pos=%lld must be >= 0", who, (long long)cur_pos); return kErrArg; }
   if (!q_fp8 || !q_s || !k_fp8 || (!PAGED && !k_s) || !w_bf16 || !logits) { set_error("%s: null pointer", who); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(k_fp8)) & 15) { set_error("%s: q and k must be 16-byte aligned", who); return kErrArg; }
