@@ -31,8 +31,11 @@ namespace tl {
 constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups per CU)
 constexpr int kDownWaves = 8;       // down waves per workgroup
 constexpr int kDownSlots = 4;  // hit experts reduced together by the down kernel
-constexpr int kDownRedBytes = sizeof(float) * kDownWaves * kDownSlots * 4 * 64;  // cross-wave partials
-constexpr int kDownTermBytes = sizeof(float) * kDownSlots * 4 * 64;              // per-slot terms
+constexpr int kDnSlots = 8;    // hit experts per batch of the LDS down kernel
+constexpr int kDnEarly = 4;    // of them copied into LDS before the hit set is known
+constexpr int kDownRedBytes = sizeof(float) * kDownWaves * kDnSlots * 4 * 64;  // cross-wave partials
+constexpr int kDownTermBytes = sizeof(float) * kDnSlots * 4 * 64;              // per-slot terms
+constexpr int kDnHBytes = 128 * 1024;  // staged h limit of the LDS down kernel (one workgroup per CU)
 constexpr int kMaxLocalExperts = 64;
 
 // Hit-expert bitmask of this shard, computed by each wave on its own (no LDS, no
@@ -110,7 +113,7 @@ __device__ inline float routing_weight(const int32_t* __restrict__ topk_idx, con
 }
 
 constexpr int kGuDepth = 2;  // weight blocks in flight per wave (gate/up, LDS activations)
-constexpr int kDnDepth = 4;  // down items in flight per wave (LDS activations)
+constexpr int kDnDepth = 2;  // down items in flight per wave (LDS activations)
 constexpr int kLdsActBytes = 64 * 1024;  // activation staging limit (2 workgroups per CU)
 
 // ------------------------------------------------------ gate/up, LDS activations
@@ -219,24 +222,28 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
     int n_local, int D, int I, int sb, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* hl = reinterpret_cast<uint16_t*>(smem);  // [sb][M][I] during the stream
-  float(*red)[kDownSlots][4][64] = reinterpret_cast<float(*)[kDownSlots][4][64]>(smem);  // after it
-  float(*term)[kDownSlots][4][64] = reinterpret_cast<float(*)[kDownSlots][4][64]>(smem + TPW * kDownRedBytes);
+  float(*red)[kDnSlots][4][64] = reinterpret_cast<float(*)[kDnSlots][4][64]>(smem);  // after it
+  float(*term)[kDnSlots][4][64] = reinterpret_cast<float(*)[kDnSlots][4][64]>(smem + TPW * kDownRedBytes);
   const int pairs = M * topk;
   const int my_e = lane_pair_expert(topk_idx, pairs, e0);
   const float my_w = lane_pair_weight(topk_w, pairs);
-  // The first batch's h rows (min(sb, n_local) slots: h holds n_local) are copied straight
-  // into LDS (global_load_lds, no registers) together with the routing loads, before the
-  // hit set is known; the copy is waited for just before the first compute.
-  const int pre16 = min(sb, n_local) * M * I / 8;
-  {
+  // The first batch's h rows are copied straight into LDS (global_load_lds, no registers):
+  // its first kDnEarly slots (h holds n_local) together with the routing loads, before the
+  // hit set is known, the rest of the batch once it is; the copy is waited for just before
+  // the first compute.
+  auto copy_h = [&](int c_begin, int c_end) {
     const int ln = threadIdx.x & 63;
-    for (int c0 = threadIdx.x - ln; c0 < pre16; c0 += blockDim.x)  // c0: this wave's first chunk
-      if (c0 + ln < pre16)
+    for (int c0 = c_begin + threadIdx.x - ln; c0 < c_end; c0 += blockDim.x)  // c0: this wave's first chunk
+      if (c0 + ln < c_end)
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(h) + c0 + ln,
                                          (lds_ptr)(smem + static_cast<size_t>(c0) * 16), 16, 0, 0);
-  }
+  };
+  const int slot16 = M * I / 8;  // 16-byte chunks per slot
+  const int early = min(min(sb, kDnEarly), n_local);
+  copy_h(0, early * slot16);
   const uint64_t mask = lane_pairs_mask(my_e, n_local);
   const int n_hit = __builtin_popcountll(mask);
+  if (n_hit > early) copy_h(early * slot16, min(n_hit, sb) * slot16);
   const int KB = I >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -250,9 +257,9 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
   for (int s0 = 0; s0 < n_hit; s0 += sb) {
     const int ns = min(sb, n_hit - s0);
     const int h16 = ns * M * I / 8;
-    v4f acc[kDownSlots];
+    v4f acc[kDnSlots];
 #pragma unroll
-    for (int j = 0; j < kDownSlots; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kDnSlots; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
     const int items = ns * KB;  // item = (slot it / KB, K block it % KB)
     const int n = wl < items ? (items - wl + kDownWaves - 1) / kDownWaves : 0;
     struct Ops {
@@ -277,7 +284,7 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
           const int j = it / KB, kb = it - j * KB;
           const ActOperand xa = lds_act(hl + (j * M + row) * I + kb * kBlock, g);
 #pragma unroll
-          for (int jj = 0; jj < kDownSlots; ++jj)
+          for (int jj = 0; jj < kDnSlots; ++jj)
             if (jj == j) acc[jj] = mfma_block_bf16(o.w, o.sc, xa, acc[jj]);
         },
         [&] {  // the batch's h rows into LDS while the first weight fetches are in flight
@@ -289,7 +296,7 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
         });
     __syncthreads();  // every wave is done with hl before it becomes the partials
 #pragma unroll
-    for (int j = 0; j < kDownSlots; ++j)
+    for (int j = 0; j < kDnSlots; ++j)
 #pragma unroll
       for (int q = 0; q < 4; ++q) red[wave][j][q][lane] = acc[j][q];
     __syncthreads();
@@ -555,14 +562,14 @@ extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, co
   if (!h_bf16 || !w2_packed || !s2 || !topk_idx || !topk_w || !y_bf16) { set_error("moe_down_combine: null pointer"); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15) { set_error("moe_down_combine: h and weights must be 16-byte aligned"); return kErrArg; }
   const int64_t h_bytes = M * I * 2;  // one hit expert's h rows
-  if (h_bytes <= kLdsActBytes && M * topk <= 64) {  // activations staged in LDS, sb hit experts per batch
-    const int sb = static_cast<int>(std::min<int64_t>(kDownSlots, kLdsActBytes / h_bytes));
+  if (h_bytes <= kDnHBytes && M * topk <= 64) {  // activations staged in LDS, sb hit experts per batch
+    const int sb = static_cast<int>(std::min<int64_t>(kDnSlots, kDnHBytes / h_bytes));
     // two output tiles per workgroup when the tile count is even: the staged h serves both
     auto launch = [&](auto tpw_tag) -> int {
       constexpr int TPW = decltype(tpw_tag)::value;
       const size_t lds = std::max<size_t>(static_cast<size_t>(sb) * h_bytes, TPW * (kDownRedBytes + kDownTermBytes));
       const void* fn = reinterpret_cast<const void*>(moe_down_lds_kernel<TPW>);
-      const int rc2 = allow_dynamic_lds(fn, static_cast<int>(std::max<size_t>(lds, kLdsActBytes)), "moe_down_combine");
+      const int rc2 = allow_dynamic_lds(fn, static_cast<int>(lds), "moe_down_combine");
       if (rc2) return rc2;
       hipLaunchKernelGGL((moe_down_lds_kernel<TPW>), dim3(D / 16 / TPW), dim3(kDownWaves * 64 * TPW), lds,
                          (hipStream_t)stream, (const uint16_t*)h_bf16, (const uint8_t*)w2_packed, s2, topk_idx, topk_w,
