@@ -32,7 +32,6 @@ constexpr int kMoeWaves = 8;        // gate/up waves per workgroup (2 workgroups
 constexpr int kDownWaves = 8;       // down waves per workgroup
 constexpr int kDownSlots = 4;  // hit experts reduced together by the down kernel
 constexpr int kDnSlots = 8;    // hit experts per batch of the LDS down kernel
-constexpr int kDnEarly = 4;    // of them copied into LDS before the hit set is known
 constexpr int kDownRedBytes = sizeof(float) * kDownWaves * kDnSlots * 4 * 64;  // cross-wave partials
 constexpr int kDownTermBytes = sizeof(float) * kDnSlots * 4 * 64;              // per-slot terms
 constexpr int kDnHBytes = 128 * 1024;  // staged h limit of the LDS down kernel (one workgroup per CU)
@@ -131,9 +130,16 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
   const int pairs = M * topk;
   const int lane = threadIdx.x & 63;
   const int raw_e = topk_idx[min(lane, pairs - 1)];
-  const int x16 = M * D / 8;
-  stage_commit(xl, stage_issue(x, x16), x16);
+  // x is copied straight into LDS (global_load_lds: no registers) once the hit set is
+  // known, and the first weight fetches are requested right after it, before it has
+  // landed; it is waited for just before the first compute.  (Issued before the routing
+  // load is consumed, the copies would be waited for there: the compiler does not count
+  // direct-to-LDS loads, so its wait for the routing load is a full vmcnt(0).)  Every
+  // thread issues the same kStageChunks copies; sources past x repeat its last chunk and
+  // their LDS destinations lie in the unused tail of the 64 KB allocation.
   const uint64_t mask = lane_pairs_mask(lane < pairs ? raw_e - e0 : -1, n_local);
+  const int x16 = M * D / 8;
+  copy_to_lds_fixed<kStageChunks>(x, x16, xl);
   const int n_hit = __builtin_popcountll(mask);
   const int KB = D >> 7;
   const int tiles = I >> 4;
@@ -142,7 +148,7 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
   const int r = lane & 15, g = lane >> 4;
   const uint16_t* xrow = xl + min(r, M - 1) * D;
   const int n = wave < KB ? (KB - wave + kMoeWaves - 1) / kMoeWaves : 0;  // K blocks wave + i*8
-  __syncthreads();
+  bool staged = false;
 
   for (int item = blockIdx.x; item < n_hit * tiles; item += gridDim.x) {
     const int slot = item / tiles, rt = item - slot * tiles;
@@ -176,6 +182,13 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
             ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wg[2 * j], o.wg[2 * j + 1], o.gs), xa, ag, 0, 0, 0);
             au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wu[2 * j], o.wu[2 * j + 1], o.us), xa, au, 0, 0, 0);
           }
+        },
+        [&] {  // first item: x has landed (this wave's copies) and is visible (barrier)
+          if (!staged) {
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            staged = true;
+          }
         });
     if (wave > 0) {
 #pragma unroll
@@ -204,6 +217,7 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
     }
     __syncthreads();
   }
+  if (!staged) __builtin_amdgcn_s_waitcnt(0);  // no item: the LDS copies land before the workgroup ends
 }
 
 // ------------------------------------------------------ down, LDS activations
@@ -227,23 +241,21 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
   const int pairs = M * topk;
   const int my_e = lane_pair_expert(topk_idx, pairs, e0);
   const float my_w = lane_pair_weight(topk_w, pairs);
-  // The first batch's h rows are copied straight into LDS (global_load_lds, no registers):
-  // its first kDnEarly slots (h holds n_local) together with the routing loads, before the
-  // hit set is known, the rest of the batch once it is; the copy is waited for just before
-  // the first compute.
-  auto copy_h = [&](int c_begin, int c_end) {
+  // The hit set first (the routing loads are waited for here), then the first batch's h
+  // rows are copied straight into LDS (global_load_lds, no registers) and the first weight
+  // fetches requested behind them; the copy is waited for just before the first compute.
+  // (Issued before the routing loads are consumed, the copies would be waited for there:
+  // the compiler does not count direct-to-LDS loads, so its wait for them is a vmcnt(0).)
+  const uint64_t mask = lane_pairs_mask(my_e, n_local);
+  const int n_hit = __builtin_popcountll(mask);
+  {
     const int ln = threadIdx.x & 63;
-    for (int c0 = c_begin + threadIdx.x - ln; c0 < c_end; c0 += blockDim.x)  // c0: this wave's first chunk
+    const int c_end = min(n_hit, sb) * M * I / 8;
+    for (int c0 = threadIdx.x - ln; c0 < c_end; c0 += blockDim.x)  // c0: this wave's first chunk
       if (c0 + ln < c_end)
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(h) + c0 + ln,
                                          (lds_ptr)(smem + static_cast<size_t>(c0) * 16), 16, 0, 0);
-  };
-  const int slot16 = M * I / 8;  // 16-byte chunks per slot
-  const int early = min(min(sb, kDnEarly), n_local);
-  copy_h(0, early * slot16);
-  const uint64_t mask = lane_pairs_mask(my_e, n_local);
-  const int n_hit = __builtin_popcountll(mask);
-  if (n_hit > early) copy_h(early * slot16, min(n_hit, sb) * slot16);
+  }
   const int KB = I >> 7;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -542,7 +554,7 @@ extern "C" int tl_moe_gate_up_swiglu(const void* x_bf16, const void* w13_packed,
   if (x_bytes <= kLdsActBytes && M * topk <= 64) {  // activations staged in LDS, routing in lanes
     rc = allow_dynamic_lds(reinterpret_cast<const void*>(moe_gate_up_lds_kernel), kLdsActBytes, "moe_gate_up_swiglu");
     if (rc) return rc;
-    hipLaunchKernelGGL(moe_gate_up_lds_kernel, dim3(grid), dim3(kMoeWaves * 64), static_cast<size_t>(x_bytes),
+    hipLaunchKernelGGL(moe_gate_up_lds_kernel, dim3(grid), dim3(kMoeWaves * 64), static_cast<size_t>(kLdsActBytes),
                        (hipStream_t)stream, (const uint16_t*)x_bf16, (const uint8_t*)w13_packed, s13, topk_idx,
                        (int)M, (int)topk, (int)expert_begin, (int)n_local, (int)D, (int)I, (uint16_t*)h_bf16);
   } else {
@@ -563,7 +575,9 @@ extern "C" int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, co
   if ((reinterpret_cast<uintptr_t>(h_bf16) | reinterpret_cast<uintptr_t>(w2_packed)) & 15) { set_error("moe_down_combine: h and weights must be 16-byte aligned"); return kErrArg; }
   const int64_t h_bytes = M * I * 2;  // one hit expert's h rows
   if (h_bytes <= kDnHBytes && M * topk <= 64) {  // activations staged in LDS, sb hit experts per batch
-    const int sb = static_cast<int>(std::min<int64_t>(kDnSlots, kDnHBytes / h_bytes));
+    // (the later batches are staged through registers: kStageChunks x 16 B per thread)
+    const int64_t stage_cap = (D / 16) % 2 == 0 ? 2 * kLdsActBytes : kLdsActBytes;
+    const int sb = static_cast<int>(std::min<int64_t>(kDnSlots, stage_cap / h_bytes));
     // two output tiles per workgroup when the tile count is even: the staged h serves both
     auto launch = [&](auto tpw_tag) -> int {
       constexpr int TPW = decltype(tpw_tag)::value;

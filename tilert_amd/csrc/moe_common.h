@@ -89,4 +89,21 @@ __device__ inline void stage_commit(void* lds, const Staged& st, int n16) {
   }
 }
 
+// Workgroup-wide direct copy of chunks [0, n16) of 16 bytes from global memory to LDS
+// (global_load_lds): every thread issues exactly F copies, chunk c = wave's first chunk +
+// lane + i * blockDim (sources past n16 repeat the last chunk), so the compiler's wait
+// counts for loads issued before the copies stay exact.  LDS destinations run up to
+// F * blockDim * 16 bytes: the caller's allocation must cover them.
+template <int F>
+__device__ inline void copy_to_lds_fixed(const void* src, int n16, void* lds) {
+  const int lane = threadIdx.x & 63;
+  const int c0 = threadIdx.x - lane;
+#pragma unroll
+  for (int i = 0; i < F; ++i) {
+    const int cw = c0 + i * static_cast<int>(blockDim.x);  // this wave's first chunk (uniform)
+    __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(src) + min(cw + lane, n16 - 1),
+                                     (lds_ptr)(static_cast<uint8_t*>(lds) + static_cast<size_t>(cw) * 16), 16, 0, 0);
+  }
+}
+
 }  // namespace tl
