@@ -33,6 +33,8 @@ def _scores_close(out, want):
     (3, 64, 2048, 2000, True),
     (8, 32, 1536, 1530, False),
     (2, 32, 300, 0, False),        # only key 0 / 0..1 visible
+    (4, 64, 70000, 69990, False),  # 8 key tiles per workgroup range
+    (3, 32, 40000, 39000, True),   # two key ranges per workgroup, masked tail
 ])
 def test_indexer_scores_vs_oracle(cuda, M, H, L, cur_pos, per_head):
     g = synth.gen(M * 100 + L)
