@@ -68,12 +68,12 @@ def test_static_matches_workspace_entry_point(cuda, first, second):
 def test_static_rejects_shapes_beyond_the_maximum(cuda):
     lib = _lib.load()
     dev = cuda
-    # stream-K at M = 256 over a long K: partials of 112 tiles x segments x 64 KB exceed 40 MiB
-    M, N, Kd = 256, 7168, 65536
+    # M = 64 over K = 655360: the GEMV's activation image (64 x K bytes + scales) exceeds 40 MiB
+    M, N, Kd = 64, 16, 655360
     a = torch.zeros(M, Kd, dtype=torch.float8_e4m3fn, device=dev)
     a_s = torch.ones(M, Kd // 128, device=dev)
     b = torch.zeros(N * Kd, dtype=torch.uint8, device=dev)
-    b_s = torch.ones(N // 128, Kd // 128, device=dev)
+    b_s = torch.ones((N + 127) // 128, Kd // 128, device=dev)
     out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
     rc = lib.tl_fp8_gemm_packed_static(a.data_ptr(), a_s.data_ptr(), b.data_ptr(), b_s.data_ptr(), out.data_ptr(),
                                        M, N, Kd, torch.cuda.current_stream(dev).cuda_stream)

@@ -26,6 +26,7 @@
 //   * M > 64 (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks staged
 //     in LDS (see below).
 #include <algorithm>
+#include <cstdint>
 #include <type_traits>
 #include <mutex>
 #include <utility>
@@ -812,8 +813,286 @@ __global__ __launch_bounds__(16 / TJ * 64) void fp8_gemm_mm_kernel(
   }
 }
 
+// Wide-tile MFMA GEMM for 64 < M <= 256 on packed weights (fp8_gemm_wide_kernel<F>).
+// A workgroup (8 waves, one workgroup per CU) owns F consecutive 16-row weight tiles x one
+// group of 8 token fragments (128 tokens) over one of S K ranges.  The host picks F (4..9)
+// and S so that tiles x token groups x S <= 256 workgroups give every CU the same work in
+// one round (up 7168 -> 18432 at M = 256: F = 9, 128 row tiles x 2 token groups; down
+// 18432 -> 7168: F = 7, 64 x 2 x 2 K ranges).  Waves w and w + 4 (one SIMD) share token
+// pair w % 4 and split the F rows, so every fragment a wave reads from LDS feeds 2 or 5
+// MFMAs and each SIMD has two waves to hide the other's latencies.
+// Per K block the weight fragments and the activation-image fragments (act_image_kernel)
+// and their scales are copied global -> LDS (global_load_lds, no registers) into a
+// 4-stage ring; each wave reads block i + 1's operands into a second register set while
+// block i's MFMAs run.  The 2F weight pieces are dealt to the waves round robin and three
+// waves copy the scales, so per-wave copy counts differ, but each wave issues the same
+// count every block and waits for its own copies with a fixed s_waitcnt before the
+// block's s_barrier.
+// Workgroup ids: the token groups of one weight slice (row tile, K range) are 8 ids apart,
+// so that, with consecutive ids dealt to the 8 XCDs round robin, both run on one XCD and
+// the second read of each weight fragment hits its L2 (FETCH_SIZE at M = 256 up: 148 MB
+// per call for 132 MB of weights).
+// With S > 1 the S partial sums of a tile are fp32 partials in the workspace, written and
+// read with 16-byte sc1 accesses (past this XCD's L2, like agent-scope atomics); the
+// workgroup that completes a tile (agent-scope counter) sums them in range order, so
+// results are deterministic.
+constexpr int kWideStages = 4;
+constexpr int kWideGrid = 256;
+constexpr int kWideTJ = 2;              // token fragments per wave
+constexpr int kWideTT = 4 * kWideTJ;    // token fragments per workgroup (4 token pairs)
+constexpr int kCpolSc1 = 16;            // buffer access cache policy: sc1
+constexpr int kRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
+
+// 8 waves: waves w and w + 4 (same SIMD) share token pair w % 4 and split the F rows
+// (FH and F - FH), so each SIMD has two waves to hide the other's LDS and MFMA latencies.
+constexpr int kWideWaves = 8;
+
+template <int F>
+struct WideShape {
+  static constexpr int FH = (F + 1) / 2;                // rows of the first split
+  static constexpr int W = F * 2048;                    // weight fragments of one K block
+  static constexpr int A = kWideTT * 2048;              // activation fragments
+  static constexpr int TS = W + A;                      // token scales (16 kWideTT floats)
+  static constexpr int WS = TS + kWideTT * 64;          // weight scales (F floats)
+  static constexpr int STAGE = WS + 256;
+  static constexpr int LDS = kWideStages * STAGE;
+  static constexpr int SLOT = F * kWideTT * 256;        // floats of one partial
+  static_assert(kWideTT * 16 == 128, "two waves copy the token scales");
+};
+
+// Copy instructions wave w issues per K block: its weight pieces (the 2F 1 KB pieces dealt
+// round robin), 2 activation pieces, and one scale copy for waves 0-1 (token scales) and
+// 2 (weight scales).
+__host__ __device__ constexpr int wide_ops(int F, int w) {
+  return (2 * F - w + kWideWaves - 1) / kWideWaves + 2 + (w < 3 ? 1 : 0);
+}
+
+// s_waitcnt needs an immediate: the wave-uniform count picks one of the possible waits
+__device__ inline void wait_vm_ops(int ops) {
+  switch (ops) {
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
+    case 10: __builtin_amdgcn_s_waitcnt(vmcnt_imm(10)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(vmcnt_imm(12)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
+  }
+}
+
+template <int F>
+__global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
+    const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
+    const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
+    uint32_t* __restrict__ counters, int M, int N, int K, int TG, int S, int per) {
+  using Sh = WideShape<F>;
+  constexpr int TJ = kWideTJ, TT = kWideTT, FH = Sh::FH;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t last_flag;
+  const int KB = K >> 7, NT = N >> 4;
+  // id -> (weight slice q, token group tg): the groups of one slice are 8 ids apart
+  const int id = static_cast<int>(blockIdx.x);
+  const int q = (id / (8 * TG)) * 8 + id % 8, tg = (id / 8) % TG;
+  if (q >= (NT / F) * S) return;  // padding ids of the last group of 8 slices
+  const int tile = q / S, seg = q % S;
+  const int kb0 = seg * per;
+  const int n = KB - kb0 < per ? KB - kb0 : per;  // >= 1 (host plan)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tp = wave & 3, rh = wave >> 2;  // token pair, row split
+  const int r = lane & 15, g = lane >> 4;
+  const int t0 = 16 * TT * tg;        // first token of the group
+  const int tf0 = TT * tg + TJ * tp;  // this wave's first token fragment
+  const int f0 = rh * FH;             // this wave's first row fragment
+  const int ops = wide_ops(F, wave);
+  const int MTT = (M + 15) >> 4;
+  // activation image fragments this wave copies: pieces wave and wave + 8 of the group
+  // (token fragments wave / 2 and 4 + wave / 2, half wave % 2; past the image's last
+  // fragment the last one is re-read, its tokens are never stored)
+  const int h = wave & 1;
+  const int ta = min(TT * tg + (wave >> 1), MTT - 1), tb = min(TT * tg + 4 + (wave >> 1), MTT - 1);
+  const int tok = min(t0 + 64 * (wave & 1) + lane, MTT * 16 - 1);  // token scales (waves 0, 1)
+  const int fr = lane < F - 1 ? lane : F - 1;
+  const float* ws_src = Bs + static_cast<size_t>((16 * (F * tile + fr)) >> 7) * KB;  // weight scales (wave 2)
+
+  // copies of K block kb into stage st
+  auto issue = [&](int kb, uint8_t* st) {
+#pragma unroll
+    for (int u = 0; u < (2 * F + kWideWaves - 1) / kWideWaves; ++u) {
+      const int p = wave + kWideWaves * u;  // fragment p / 2, half p % 2
+      if (p < 2 * F)
+        copy_to_lds16(B + packed_fragment(F * tile + (p >> 1), kb, NT) + (p & 1) * 1024 + lane * 16, st + p * 1024);
+    }
+    const uint8_t* xk = X + static_cast<size_t>(kb) * MTT * 2048 + h * 1024 + lane * 16;
+    copy_to_lds16(xk + ta * 2048, st + Sh::W + wave * 1024);
+    copy_to_lds16(xk + tb * 2048, st + Sh::W + (8 + wave) * 1024);
+    if (wave < 2) copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + Sh::TS + 256 * wave);
+    else if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
+  };
+
+  v4f acc[FH][TJ];
+#pragma unroll
+  for (int f = 0; f < FH; ++f)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[f][j] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  // Operands of one K block for rows f0 .. f0 + NR - 1, read from LDS into registers.
+  // The loop is software-pipelined over two such sets: block i + 1's fragments are read
+  // while block i's MFMAs run, so LDS reads and matrix work overlap.
+  auto run = [&](auto nr_tag) {
+    constexpr int NR = decltype(nr_tag)::value;
+    struct Ops {
+      v8i a[TJ], w[NR];
+      float ts[TJ], ws[NR];
+    };
+    auto load = [&](const uint8_t* st, Ops& o) {
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) o.a[j] = load_fragment(st + Sh::W + (TJ * tp + j) * 2048, lane);
+#pragma unroll
+      for (int f = 0; f < NR; ++f) o.w[f] = load_fragment(st + (f0 + f) * 2048, lane);
+      const float* tsr = reinterpret_cast<const float*>(st + Sh::TS) + 16 * TJ * tp;
+      const float* wsr = reinterpret_cast<const float*>(st + Sh::WS) + f0;
+#pragma unroll
+      for (int j = 0; j < TJ; ++j) o.ts[j] = tsr[16 * j + r];
+#pragma unroll
+      for (int f = 0; f < NR; ++f) o.ws[f] = wsr[f];
+    };
+    // all MFMAs first, then the scaled accumulation (independent products issue back to back)
+    auto mma = [&](const Ops& o) {
+      v4f pr[NR][TJ];
+#pragma unroll
+      for (int f = 0; f < NR; ++f)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j)
+          pr[f][j] = mfma_16x16x128_fp8(o.w[f], o.a[j]);
+#pragma unroll
+      for (int f = 0; f < NR; ++f)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[f][j] += pr[f][j] * (o.ts[j] * o.ws[f]);
+    };
+    auto stage = [&](int i) { return smem + (i & 3) * Sh::STAGE; };
+    auto last = [&](int i) { return kb0 + (i < n - 1 ? i : n - 1); };  // past the range: re-copy the last block
+    // Ring of 4 stages.  Iteration i: wait for block i + 1's copies (this wave's; the
+    // barrier then covers every wave's), read them into the other register set, copy
+    // block i + 3 into the stage block i - 1 used (its reads finished in iteration i - 2),
+    // and multiply block i.  Each wave always has the same number of its copies in
+    // flight, so the wait counts are fixed.
+    static_assert(kWideStages == 4, "wait counts below assume 4 stages");
+    issue(last(0), stage(0));
+    issue(last(1), stage(1));
+    issue(last(2), stage(2));
+    wait_vm_ops(2 * ops);
+    asm volatile("s_barrier" ::: "memory");
+    Ops o0, o1;
+    load(stage(0), o0);
+    auto step = [&](int i, const Ops& cur, Ops& nxt) {
+      wait_vm_ops(ops);
+      asm volatile("s_barrier" ::: "memory");
+      issue(last(i + 3), stage(i + 3));
+      load(stage(i + 1), nxt);  // unconditional (past the range it reads a stage unused): no
+      mma(cur);                 // branch, so the wait for cur's reads stays partial
+    };
+    for (int i = 0; i < n; i += 2) {
+      step(i, o0, o1);
+      if (i + 1 < n) step(i + 1, o1, o0);
+    }
+  };
+  if (rh == 0) run(std::integral_constant<int, FH>{});
+  else run(std::integral_constant<int, F - FH>{});
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the workgroup ends
+
+  // lane holds rows 16 (F tile + f0 + f) + 4 g + (0..3) of token 16 (tf0 + j) + r
+  const int nrows = rh == 0 ? FH : F - FH;
+  auto token = [&](int j) { return 16 * (tf0 + j) + r; };
+  auto column = [&](int f) { return 16 * (F * tile + f0 + f) + 4 * g; };
+  auto store_all = [&]() {
+#pragma unroll
+    for (int f = 0; f < FH; ++f)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        if (f < nrows && token(j) < M) store_out(out, token(j), column(f), pack_bf16x4(acc[f][j]));
+  };
+  if (S == 1) {
+    store_all();
+    return;
+  }
+  // partial of (tile, tg, seg): [row fragment][token fragment of the group][lane][4] fp32
+  typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+  const int slot_bytes = Sh::SLOT * 4;
+  const size_t tile_slots = (static_cast<size_t>(tile) * TG + tg) * S;
+  auto off = [&](int f, int j) { return (((f0 + f) * TT + TJ * tp + j) * 64 + lane) * 16; };
+  {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(partial + (tile_slots + seg) * Sh::SLOT, 0, slot_bytes, kRsrcWord3);
+#pragma unroll
+    for (int f = 0; f < FH; ++f)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        if (f < nrows)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4v, acc[f][j]), rs, off(f, j), 0, kCpolSc1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    last_flag = __hip_atomic_fetch_add(&counters[tile * TG + tg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                static_cast<uint32_t>(S - 1);
+  __syncthreads();
+  if (!last_flag) return;
+#pragma unroll
+  for (int f = 0; f < FH; ++f)
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) acc[f][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int sq = 0; sq < S; ++sq) {  // ranges in K order
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(partial + (tile_slots + sq) * Sh::SLOT, 0, slot_bytes, kRsrcWord3);
+#pragma unroll
+    for (int f = 0; f < FH; ++f)
+#pragma unroll
+      for (int j = 0; j < TJ; ++j)
+        if (f < nrows)
+          acc[f][j] += __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, off(f, j), 0, kCpolSc1));
+  }
+  store_all();
+  if (tid == 0) __hip_atomic_store(&counters[tile * TG + tg], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Plan of the wide kernel: F (row tiles per workgroup, 4..9, dividing N / 16) and the K
+// split S minimising rounds x F x (K blocks per range) -- the MFMA work of the busiest CU
+// -- with at most 256 workgroups per round (token groups x tiles x S); ties go to fewer
+// K ranges.  F = 0: no F divides N / 16.
+struct WidePlan {
+  int F, TG, S, per, tiles;
+  int grid() const { return static_cast<int>(cdiv(static_cast<int64_t>(tiles) * S, 8)) * 8 * TG; }
+};
+
+__host__ inline WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
+  const int NT = static_cast<int>(N / 16), KB = static_cast<int>(K / kBlock);
+  const int TG = static_cast<int>(cdiv(cdiv(M, 16), kWideTT));
+  WidePlan best{0, TG, 1, KB, 0};
+  int64_t best_cost = INT64_MAX;
+  for (int F = 9; F >= 4; --F) {
+    if (NT % F) continue;
+    const int tiles = NT / F;
+    int S = std::max(1, std::min(KB, kWideGrid / (tiles * TG)));
+    const int per = static_cast<int>(cdiv(KB, S));
+    S = static_cast<int>(cdiv(KB, per));
+    const int64_t cost = cdiv(static_cast<int64_t>(tiles) * TG * S, kWideGrid) * F * per * 16 + (S - 1);
+    if (cost < best_cost) { best_cost = cost; best = WidePlan{F, TG, S, per, tiles}; }
+  }
+  return best;
+}
+
+__host__ inline size_t wide_partial_bytes(int64_t M, int64_t N, int64_t K) {
+  const WidePlan w = plan_wide(M, N, K);
+  if (w.S == 1) return 0;
+  return static_cast<size_t>(w.tiles) * w.TG * w.S * w.F * kWideTT * 256 * sizeof(float);
+}
+
+
 struct GemmPlan {
-  bool mm;     // M > 64, packed weight: fp8_gemm_mm_kernel
+  bool mm;     // M > 64, packed weight: fp8_gemm_wide_kernel (or fp8_gemm_mm_kernel)
+  bool wide;   // ... the wide kernel (some F in 4..9 divides N / 16)
   bool tiled;  // M > 64, canonical weight: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
@@ -841,7 +1120,8 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   p.depth = 2;
   p.rt = 1;
   p.xf = false;
-  if (p.mm) {  // stream-K over 128 x 128 tiles, one workgroup per CU
+  p.wide = p.mm && plan_wide(M, N, K).F > 0;
+  if (p.mm) {  // the wide kernel, else stream-K over 128 x 128 tiles (activation image)
     p.row_groups = kMmGrid;
     p.ksplit = 1;
     p.kb_per_split = KB;
@@ -895,6 +1175,7 @@ constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 
 // Workspace: counters, then the split-K partials, then the activation image (256-aligned).
 static size_t mm_partial_bytes(int64_t M, int64_t N, int64_t K) {
+  if (plan_wide(M, N, K).F > 0) return wide_partial_bytes(M, N, K);
   const int64_t tiles = (N / 128) * cdiv(M, 128), KB = K / kBlock;
   const int G = mm_grid(tiles, tiles * KB);
   if (G == tiles) return 0;  // a whole tile per workgroup: no partials
@@ -926,6 +1207,28 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
                        A, As, img, img_s, M, K);
     xa = img;
     xsa = img_s;
+  }
+  if (p.wide) {
+    uint32_t* cnt = static_cast<uint32_t*>(workspace);
+    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    const WidePlan w = plan_wide(M, N, K);
+    auto go = [&](auto f_tag) -> int {
+      constexpr int F_ = decltype(f_tag)::value;
+      constexpr int lds = WideShape<F_>::LDS;
+      const void* fn = reinterpret_cast<const void*>(fp8_gemm_wide_kernel<F_>);
+      if (const int rc = allow_dynamic_lds(fn, lds, "fp8_gemm")) return rc;
+      hipLaunchKernelGGL(fp8_gemm_wide_kernel<F_>, dim3(w.grid()), dim3(kWideWaves * 64), lds, st, xa, xsa, B, Bs, out,
+                         part, cnt, M, N, K, w.TG, w.S, w.per);
+      return check_launch("fp8_gemm");
+    };
+    switch (w.F) {
+      case 9: return go(std::integral_constant<int, 9>{});
+      case 8: return go(std::integral_constant<int, 8>{});
+      case 7: return go(std::integral_constant<int, 7>{});
+      case 6: return go(std::integral_constant<int, 6>{});
+      case 5: return go(std::integral_constant<int, 5>{});
+      default: return go(std::integral_constant<int, 4>{});
+    }
   }
   if (p.mm) {
     uint32_t* cnt = static_cast<uint32_t*>(workspace);
