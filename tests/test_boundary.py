@@ -60,7 +60,7 @@ def test_argument_errors_need_no_gpu():
     assert lib.tl_fp8_gemm_workspace_bytes(32, 576, 7168) > 0  # narrow layer at M > 16: split K
     # the allocation-free GEMM rejects a shape whose scratch exceeds its static array before
     # touching the device (pointers are only checked for null and alignment)
-    assert lib.tl_fp8_gemm_packed_static(256, 256, 256, 256, 256, 256, 7168, 65536, None) == 3
+    assert lib.tl_fp8_gemm_packed_static(256, 256, 256, 256, 256, 64, 16, 655360, None) == 3
     assert b"static maximum" in lib.tl_last_error()
     assert lib.tl_fp8_gemm_workspace_bytes(4, 576, 7168) == 0  # GEMV: never split
     assert lib.tl_fp8_gemm_workspace_bytes(4, 18432, 7168) == 0
