@@ -4,9 +4,10 @@ projx_wqkva.py:503-529):
 
 * config 0: one linear 7168 -> 18432 at M = 1, seed 0;
 * config 3: the dense MLP's up 7168 -> 18432 and down 18432 -> 7168 at
-  M in {1, 4, 16, 64, 256} (seeds 1..5), on both weight layouts.  At M = 256 the up
-  projection has 288 output tiles, so the one-tile-per-workgroup MFMA GEMM runs; the down
-  projection (112 tiles) runs the stream-K schedule; M <= 64 runs the GEMV.
+  M in {1, 4, 16, 64, 256} (seeds 1..5), on both weight layouts.  On packed weights M = 64
+  and 256 run the wide MFMA GEMM (up: 128 slices of 9 row tiles x 2 token groups at M =
+  256; down: 64 slices of 7 row tiles split over K), canonical weights run the GEMV at
+  M <= 64 and the tiled kernel at M = 256; M <= 16 runs the GEMV on both.
 
 The bar is the workload's: relative L2 <= 5e-3 and max-abs <= 2 bf16 ulp of the output
 scale (``tests/_tol.py``).
@@ -51,7 +52,7 @@ class _Layer:
         assert_gemm_close(out_c, want, "canonical " + what)
         assert_gemm_close(out_p, want, "packed " + what)
         assert torch.equal(out_p, out_p2), "packed GEMM not deterministic: " + what
-        if M <= 64:  # the same GEMV on both layouts
+        if M <= 32:  # the same GEMV on both layouts
             assert torch.equal(out_c, out_p), "layouts differ: " + what
 
 

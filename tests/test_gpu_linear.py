@@ -71,7 +71,7 @@ GEMM_CASES = [
     (17, 512, 1024),
     (64, 1024, 2048),
     (256, 512, 1024),
-    (64, 2048, 7168),   # per-row-tile kernel, 4 token tiles, split-K
+    (64, 2048, 7168),   # canonical: per-row-tile kernel, 4 token tiles, split-K; packed: wide kernel
     (128, 2048, 7168),  # tiled kernel (M > 64) with split-K
     (32, 1152, 2048),
     (200, 400, 2048),   # 25 row tiles: a partly empty last 128-row group
@@ -83,9 +83,10 @@ GEMM_CASES = [
     (24, 6144, 512),    # 2 row tiles, 2 token tiles
     (48, 7168, 1024),   # 2 row tiles, 4 token tiles
     (64, 12288, 512),   # 4 row tiles, 4 token tiles
-    # M > 64, packed: stream-K MFMA GEMM
-    (65, 128, 512),     # one tile of 4 K blocks over 4 workgroups: 4 partials
-    (192, 1024, 2048),  # 16 tiles x 16 blocks over 256 workgroups: 1-unit ranges, a half-full token group
+    # M > 32, packed: wide MFMA GEMM
+    (65, 128, 512),     # one 8-row-tile slice split over all 4 K blocks: 4 partials
+    (192, 1024, 2048),  # 2 token groups, the second half full; 8 tiles x 16 K ranges
+    (40, 2048, 1024),   # one token group with 3 of its 8 fragments past M
 ]
 
 
@@ -104,9 +105,9 @@ def test_fp8_gemm_vs_oracle(cuda, M, N, Kd):
     if Kd % 512 == 0:
         packed = K.pack_weight(wq.to(cuda), ws.to(cuda))
         outp = K.fp8_gemm(xq.to(cuda), xs.to(cuda), packed)
-        if M <= 64:  # the same GEMV kernel on both layouts
+        if M <= 32 or N % 128:  # the same GEMV kernel on both layouts
             assert torch.equal(outp, out), "packed-weight GEMM differs from the canonical one"
-        else:  # M > 64: the MFMA GEMM (packed) and the tiled kernel (canonical) sum differently
+        else:  # the wide MFMA GEMM (packed) and the GEMV / tiled kernel (canonical) sum differently
             assert torch.equal(outp, K.fp8_gemm(xq.to(cuda), xs.to(cuda), packed)), "not deterministic"
             assert_gemm_close(outp, ref.fp8_gemm(xq, xs, wq, ws), f"packed M={M} N={N} K={Kd}")
 
@@ -175,5 +176,5 @@ def test_fp8_gemm_split_k_repeatable(cuda, M, N, Kd):
     torch.cuda.synchronize()
     for o in outs:
         assert torch.equal(o, first)
-    for o in outs_c:  # M > 64: another kernel for the canonical layout, also deterministic
-        assert torch.equal(o, first if M <= 64 else first_c)
+    for o in outs_c:  # packed M > 32 with N % 128 = 0: the wide kernel; canonical: another one
+        assert torch.equal(o, first if (M <= 32 or N % 128) else first_c)

@@ -17,14 +17,17 @@
 //     each wave-wide load reads 1 KB of consecutive memory.  Packing is done once at
 //     weight-load time (tl_fp8_pack_weight), like the reference's per-op weight
 //     converters.  Measured on MI355X: packed fragments stream ~25% faster.
-//   * M <= 64 (fp8_gemm_kernel): a workgroup owns one 16-row tile and a slice of K blocks;
+//   * M <= 64 (fp8_gemm_kernel; M <= 32 on packed weights with N % 128 = 0): a workgroup
+//     owns one 16-row tile and a slice of K blocks;
 //     its 4-8 waves interleave over the slice, each with the next block's operands in
 //     flight (two buffers in ping-pong; deeper rings measured no faster), and are summed
 //     through LDS in a fixed order.  The K split is chosen so the grid covers the 256 CUs
 //     evenly; the last workgroup of a row tile (agent-scope counter and agent-scope atomic
 //     partials) sums the fp32 partials in slice order, so results are deterministic.
-//   * M > 64 (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks staged
-//     in LDS (see below).
+//   * M > 32 on packed weights with N % 128 = 0 (fp8_gemm_wide_kernel): F row tiles x 128
+//     tokens per workgroup, one balanced round of 256 workgroups, operands staged in LDS.
+//   * M > 64 otherwise (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks
+//     staged in LDS (see below).
 #include <algorithm>
 #include <cstdint>
 #include <type_traits>
@@ -589,231 +592,8 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
   if (tid == 0) __hip_atomic_store(&counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---------------------------------------------------------------- M > 64: MFMA GEMM
-// Output tiles are 128 weight rows (one scale block) x 128 tokens.  Per K block, both
-// operands -- 8 packed weight fragments and 8 fragments of the activation image, 2 KB of
-// consecutive memory each -- plus the block's 128 token scales and its weight scale are
-// copied global -> LDS by the load-to-LDS path (no registers), into a ring of S stages:
-// the copies of block i + S - 1 are issued while block i is computed.  The waves form a
-// 2 x (8 / TJ) grid over the tile: each holds 4 row tiles x TJ token tiles of
-// accumulators (4 TJ MFMAs per K block from 4 + TJ fragments read from LDS).
-//
-// Two schedules (SK):
-//  * at >= 256 tiles, one tile per workgroup: S = 2 stages (67 KB), 4 waves (TJ = 4), two
-//    workgroups per CU, so that one's copies overlap the other's MFMAs;
-//  * below that, "stream-K": the work -- tiles x K blocks, tile-major -- is cut into one
-//    equal contiguous range per CU (256 workgroups, S = 4 stages of 134 KB, 8 waves, TJ =
-//    2).  A range covers a few tile segments; a segment that is a whole tile is stored
-//    directly, others publish fp32 partials and the segment that completes a tile sums
-//    the tile's partials in K order (deterministic).
-// Measured (MI355X, up 7168 -> 18432 / down 18432 -> 7168): M = 256 81 / 91 us, M = 128
-// 73 / 81 us; the per-row-tile tiled kernel before it took 268 / 374 and 143 / ~180 us.
-// What bounds it now is latency, not a unit: the MFMA pipe is busy 17% of the time
-// (SQ_VALU_MFMA_BUSY_CYCLES), waves wait on memory counters ~40%, and each K block costs a
-// workgroup barrier.
-constexpr int kMmStageBytes = 32768 + 512 + 256;  // weights, activations, token scales, weight scale
-constexpr int kMmGrid = 256;  // stream-K: one workgroup per CU
-
-// Stream-K schedule: workgroup g owns work units [g U / G, (g+1) U / G).
-struct MmSched {
-  int64_t U;  // tiles * KB
-  int G;
-  __host__ __device__ int64_t start(int g) const { return static_cast<int64_t>(g) * U / G; }
-  __host__ __device__ int owner(int64_t u) const {  // the g whose range holds u
-    int g = static_cast<int>(u * G / U);
-    while (g + 1 < G && start(g + 1) <= u) ++g;
-    while (g > 0 && start(g) > u) --g;
-    return g;
-  }
-};
-
-// Workgroups: one per CU, but never more than units, so that no range is empty (the
-// segment numbering below counts consecutive workgroups).
-// At >= 256 tiles, one tile per workgroup (two workgroups fit per CU with the short ring,
-// measured faster than stream-K there: 75 vs 98 us at 256 x 18432 x 7168).
-__host__ inline int mm_grid(int64_t tiles, int64_t U) {
-  if (tiles >= kMmGrid) return static_cast<int>(tiles);
-  return static_cast<int>(std::min<int64_t>(kMmGrid, U));
-}
-
-// Partial slots per tile: a tile of KB units meets at most this many workgroup ranges.
-__host__ inline int mm_max_segments(int64_t U, int G, int KB) {
-  const int64_t per = U / G;  // shortest range
-  return static_cast<int>(per > 0 ? cdiv(KB, per) + 1 : KB);
-}
-
-template <int S, int TJ, bool SK>
-__global__ __launch_bounds__(16 / TJ * 64) void fp8_gemm_mm_kernel(
-    const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
-    const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
-    uint32_t* __restrict__ counters, int M, int N, int K, int max_seg) {
-  // One LDS array per ring stage: the operand reads of one stage then provably never
-  // alias the copies into another.
-  __shared__ __attribute__((aligned(16))) uint8_t stage0[kMmStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t stage1[kMmStageBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t stage2[S > 2 ? kMmStageBytes : 16];
-  __shared__ __attribute__((aligned(16))) uint8_t stage3[S > 3 ? kMmStageBytes : 16];
-  __shared__ uint32_t last_flag;
-  static_assert(S >= 2 && S <= 4, "ring depth");
-  const int KB = K >> 7, NT = N >> 4, MTT = (M + 15) >> 4;
-  const int NB = N >> 7;
-  const int tiles = NB * static_cast<int>((M + 127) >> 7);
-  const MmSched sched{static_cast<int64_t>(tiles) * KB, static_cast<int>(gridDim.x)};
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, g = lane >> 4;
-  constexpr int FPW = TJ / 2;               // weight (and activation) fragments each wave copies
-  constexpr int OPS = 4 * FPW + 2;          // copy instructions per wave per stage
-  const int wn = wave & 1, wm = wave >> 1;  // rows 64 wn.., tokens 16 TJ wm..
-
-  auto stage = [&](auto b) -> uint8_t* {
-    constexpr int B_ = decltype(b)::value;
-    return B_ == 0 ? stage0 : (B_ == 1 ? stage1 : (B_ == 2 ? stage2 : stage3));
-  };
-
-  const int64_t u_end = sched.start(blockIdx.x + 1);
-  for (int64_t u = sched.start(blockIdx.x); u < u_end;) {
-    const int tile = static_cast<int>(u / KB);
-    const int kb0 = static_cast<int>(u % KB);
-    const int n = static_cast<int>(min(static_cast<int64_t>(KB - kb0), u_end - u));
-    const int nb = tile % NB, mg = tile / NB;
-
-    // copies of K block kb of this tile into stage buffer st
-    auto issue = [&](int kb, uint8_t* st) {
-#pragma unroll
-      for (int u = 0; u < FPW; ++u) {
-        const int f = FPW * wave + u;  // weight and activation fragments f of this wave
-        const uint8_t* w = B + packed_fragment(8 * nb + f, kb, NT) + lane * 16;
-        const uint8_t* x = X + (static_cast<size_t>(kb) * MTT + min(8 * mg + f, MTT - 1)) * 2048 + lane * 16;
-        copy_to_lds16(w, st + f * 2048);
-        copy_to_lds16(w + 1024, st + f * 2048 + 1024);
-        copy_to_lds16(x, st + 16384 + f * 2048);
-        copy_to_lds16(x + 1024, st + 16384 + f * 2048 + 1024);
-      }
-      // token scales: wave w copies tokens 64 (w & 1) .. +63 of the group (pairs of waves
-      // write the same bytes); past the image's last token the index is clamped (never stored)
-      const int tok = min(128 * mg + 64 * (wave & 1) + lane, MTT * 16 - 1);
-      copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + 32768 + 256 * (wave & 1));
-      copy_to_lds4(Bs + static_cast<size_t>(nb) * KB + kb, st + 32768 + 512);
-    };
-
-    v4f acc[4][TJ];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    auto compute = [&](const uint8_t* st) {
-      v8i wf[4], xf[TJ];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint4 lo = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + lane * 16);
-        const uint4 hi = *reinterpret_cast<const uint4*>(st + (4 * wn + i) * 2048 + 1024 + lane * 16);
-        wf[i] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-      }
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) {
-        const uint4 lo = *reinterpret_cast<const uint4*>(st + 16384 + (TJ * wm + j) * 2048 + lane * 16);
-        const uint4 hi = *reinterpret_cast<const uint4*>(st + 16384 + (TJ * wm + j) * 2048 + 1024 + lane * 16);
-        xf[j] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-      }
-      const float bs = *reinterpret_cast<const float*>(st + 32768 + 512);
-      float sc[TJ];
-#pragma unroll
-      for (int j = 0; j < TJ; ++j) sc[j] = reinterpret_cast<const float*>(st + 32768)[16 * TJ * wm + 16 * j + r] * bs;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) acc[i][j] += mfma_16x16x128_fp8(wf[i], xf[j]) * sc[j];
-    };
-
-    // ring: copies run S - 1 blocks ahead; past the segment the last block is re-copied,
-    // so every wave always has the same number of copies in flight (a fixed wait count)
-    __syncthreads();  // the previous segment's last reads of every stage are done
-    static_for<S - 1>([&](auto j) { issue(kb0 + min(static_cast<int>(decltype(j)::value), n - 1), stage(j)); });
-    for (int i0 = 0; i0 < n; i0 += S) {
-      static_for<S>([&](auto jj) {
-        constexpr int J = decltype(jj)::value;
-        const int i = i0 + J;
-        if (i < n) {
-          __builtin_amdgcn_s_waitcnt(vmcnt_imm((S - 2) * OPS));  // block i's copies (this wave's) landed
-          asm volatile("s_barrier" ::: "memory");                   // ... and every wave's
-          // into the stage block i - 1 used, which every wave has finished
-          issue(kb0 + min(i + S - 1, n - 1), stage(std::integral_constant<int, (J + S - 1) % S>{}));
-          compute(stage(std::integral_constant<int, J>{}));
-        }
-      });
-    }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the stages are reused
-    // lane holds rows 128 nb + 16 (4 wn + i) + 4 g + (0..3) of token 128 mg + 64 wm + 16 j + r
-    auto token = [&](int j) { return 128 * mg + 16 * TJ * wm + 16 * j + r; };
-    auto column = [&](int i) { return 128 * nb + 16 * (4 * wn + i) + 4 * g; };
-    if (!SK || n == KB) {  // the whole tile (always, without stream-K)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j)
-          if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(acc[i][j]));
-    } else {
-      // segment seg of the tile: fp32 partial into slot (tile, seg), agent-scope stores
-      const int64_t tile_u0 = static_cast<int64_t>(tile) * KB;
-      const int first = sched.owner(tile_u0);
-      const int seg = static_cast<int>(blockIdx.x) - first;
-      const int nseg = sched.owner(tile_u0 + KB - 1) - first + 1;
-      float* slot = partial + (static_cast<size_t>(tile) * max_seg + seg) * 16384;
-      // slot layout: [row tile i8 0..7][token tile j8 0..7][v4f per lane]
-      auto slot_off = [&](float* base, int i, int j) {
-        return base + ((static_cast<size_t>(4 * wn + i) * 8 + (TJ * wm + j)) * 64 + lane) * 4;
-      };
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-          float* d = slot_off(slot, i, j);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) __hip_atomic_store(d + e, acc[i][j][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      if (tid == 0)
-        last_flag = __hip_atomic_fetch_add(&counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                    static_cast<uint32_t>(nseg - 1);
-      __syncthreads();
-      if (last_flag) {
-        v4f (&sum)[4][TJ] = acc;  // this segment's own partial is in its slot now
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < TJ; ++j) sum[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
-        for (int q = 0; q < nseg; ++q) {  // segments in K order
-          float* src = partial + (static_cast<size_t>(tile) * max_seg + q) * 16384;
-          v4f v[4][TJ];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-              const float* s_ = slot_off(src, i, j);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[i][j][e] = __hip_atomic_load(s_ + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) sum[i][j] += v[i][j];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int j = 0; j < TJ; ++j)
-            if (token(j) < M) store_out(out, token(j), column(i), pack_bf16x4(sum[i][j]));
-        if (tid == 0) __hip_atomic_store(&counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    u += n;
-  }
-}
-
-// Wide-tile MFMA GEMM for 64 < M <= 256 on packed weights (fp8_gemm_wide_kernel<F>).
+// ---------------------------------------------------------------- M > 32: MFMA GEMM
+// Wide-tile MFMA GEMM for 32 < M <= 256 on packed weights (fp8_gemm_wide_kernel<F>).
 // A workgroup (8 waves, one workgroup per CU) owns F consecutive 16-row weight tiles x one
 // group of 8 token fragments (128 tokens) over one of S K ranges.  The host picks F (4..9)
 // and S so that tiles x token groups x S <= 256 workgroups give every CU the same work in
@@ -837,6 +617,10 @@ __global__ __launch_bounds__(16 / TJ * 64) void fp8_gemm_mm_kernel(
 // workgroup that completes a tile (agent-scope counter) sums them in range order, so
 // results are deterministic.
 constexpr int kWideStages = 4;
+// From M = 33 on the wide kernel beats the GEMV on packed weights (measured: up 7168 ->
+// 18432 at M = 33 / 48 / 64: 37.9 / 38.8 / 38.9 vs 48.9 / 49.1 / 51.2 us; down 18432 ->
+// 7168 level at ~40 us); at M = 17 the GEMV is faster (35.7 vs 37.4 us).
+constexpr int kWideMinM = 32;
 constexpr int kWideGrid = 256;
 constexpr int kWideTJ = 2;              // token fragments per wave
 constexpr int kWideTT = 4 * kWideTJ;    // token fragments per workgroup (4 token pairs)
@@ -1091,8 +875,7 @@ __host__ inline size_t wide_partial_bytes(int64_t M, int64_t N, int64_t K) {
 
 
 struct GemmPlan {
-  bool mm;     // M > 64, packed weight: fp8_gemm_wide_kernel (or fp8_gemm_mm_kernel)
-  bool wide;   // ... the wide kernel (some F in 4..9 divides N / 16)
+  bool mm;     // M > 32, packed weight, N % 128 = 0: fp8_gemm_wide_kernel
   bool tiled;  // M > 64, canonical weight: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
@@ -1115,17 +898,16 @@ struct GemmPlan {
 static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
-  p.mm = M > 64 && packed && N % 128 == 0 && K % (kBlock * kGroup) == 0;
+  p.mm = M > kWideMinM && packed && N % 128 == 0 && K % (kBlock * kGroup) == 0;
   p.tiled = M > 64 && !p.mm;
   p.depth = 2;
   p.rt = 1;
   p.xf = false;
-  p.wide = p.mm && plan_wide(M, N, K).F > 0;
-  if (p.mm) {  // the wide kernel, else stream-K over 128 x 128 tiles (activation image)
-    p.row_groups = kMmGrid;
+  if (p.mm) {  // the wide kernel (N % 128 = 0: F = 8 always divides N / 16)
+    p.row_groups = 0;
     p.ksplit = 1;
     p.kb_per_split = KB;
-    p.waves = 8;
+    p.waves = kWideWaves;
     p.xf = true;
     return p;
   }
@@ -1174,16 +956,9 @@ constexpr int kMaxRowTiles = 16384;  // N <= 262144
 constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
 
 // Workspace: counters, then the split-K partials, then the activation image (256-aligned).
-static size_t mm_partial_bytes(int64_t M, int64_t N, int64_t K) {
-  if (plan_wide(M, N, K).F > 0) return wide_partial_bytes(M, N, K);
-  const int64_t tiles = (N / 128) * cdiv(M, 128), KB = K / kBlock;
-  const int G = mm_grid(tiles, tiles * KB);
-  if (G == tiles) return 0;  // a whole tile per workgroup: no partials
-  return static_cast<size_t>(tiles) * mm_max_segments(tiles * KB, G, static_cast<int>(KB)) * 16384 * sizeof(float);
-}
 
 static size_t image_offset(const GemmPlan& p, int64_t M, int64_t N, int64_t K) {
-  const size_t partial = p.mm ? mm_partial_bytes(M, N, K)
+  const size_t partial = p.mm ? wide_partial_bytes(M, N, K)
                               : (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * M * N * sizeof(float) : 0);
   return kCounterBytes + (partial + 255) / 256 * 256;
 }
@@ -1208,7 +983,7 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
     xa = img;
     xsa = img_s;
   }
-  if (p.wide) {
+  if (p.mm) {
     uint32_t* cnt = static_cast<uint32_t*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     const WidePlan w = plan_wide(M, N, K);
@@ -1229,21 +1004,6 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
       case 5: return go(std::integral_constant<int, 5>{});
       default: return go(std::integral_constant<int, 4>{});
     }
-  }
-  if (p.mm) {
-    uint32_t* cnt = static_cast<uint32_t*>(workspace);
-    float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
-    const int64_t tiles = (N / 128) * cdiv(M, 128), U = tiles * (K / kBlock);
-    const int G = mm_grid(tiles, U);
-    const int max_seg = mm_max_segments(U, G, K / kBlock);
-    if (G == tiles) {  // a whole tile per workgroup, 2 workgroups per CU: 2-stage ring of 67 KB, 4 waves
-      hipLaunchKernelGGL((fp8_gemm_mm_kernel<2, 4, false>), dim3(G), dim3(4 * 64), 0, st, xa, xsa, B, Bs, out, part, cnt, M, N,
-                         K, max_seg);
-    } else {  // stream-K, 1 workgroup per CU: 4-stage ring of 134 KB, 8 waves
-      hipLaunchKernelGGL((fp8_gemm_mm_kernel<4, 2, true>), dim3(G), dim3(8 * 64), 0, st, xa, xsa, B, Bs, out, part, cnt, M, N,
-                         K, max_seg);
-    }
-    return check_launch("fp8_gemm");
   }
   if (p.tiled) {
     auto launch = [&](auto tt_tag) -> int {
