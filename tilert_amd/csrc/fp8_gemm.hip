@@ -601,9 +601,9 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 // 18432 -> 7168: F = 7, 64 x 2 x 2 K ranges).  Waves w and w + 4 (one SIMD) share token
 // pair w % 4 and split the F rows, so every fragment a wave reads from LDS feeds 2 or 5
 // MFMAs and each SIMD has two waves to hide the other's latencies.
-// Per K block the weight fragments and the activation-image fragments (act_image_kernel)
-// and their scales are copied global -> LDS (global_load_lds, no registers) into a
-// 4-stage ring; each wave reads block i + 1's operands into a second register set while
+// Per K block the weight fragments, the activation rows (read from x [M, K] itself) and
+// their scales are copied global -> LDS (global_load_lds, no registers) into a 4-stage
+// ring; each wave reads block i + 1's operands into a second register set while
 // block i's MFMAs run.  The 2F weight pieces are dealt to the waves round robin and three
 // waves copy the scales, so per-wave copy counts differ, but each wave issues the same
 // count every block and waits for its own copies with a fixed s_waitcnt before the
@@ -670,6 +670,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int TG, int S, int per) {
+  // X [M, K] e4m3fn and Xs [M, K / 128] fp32: the activations and their scales
   using Sh = WideShape<F>;
   constexpr int TJ = kWideTJ, TT = kWideTT, FH = Sh::FH;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -690,13 +691,17 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   const int tf0 = TT * tg + TJ * tp;  // this wave's first token fragment
   const int f0 = rh * FH;             // this wave's first row fragment
   const int ops = wide_ops(F, wave);
-  const int MTT = (M + 15) >> 4;
-  // activation image fragments this wave copies: pieces wave and wave + 8 of the group
-  // (token fragments wave / 2 and 4 + wave / 2, half wave % 2; past the image's last
-  // fragment the last one is re-read, its tokens are never stored)
-  const int h = wave & 1;
-  const int ta = min(TT * tg + (wave >> 1), MTT - 1), tb = min(TT * tg + 4 + (wave >> 1), MTT - 1);
-  const int tok = min(t0 + 64 * (wave & 1) + lane, MTT * 16 - 1);  // token scales (waves 0, 1)
+  // Activations straight from x [M, K] (no image pass).  Piece p of the group (waves copy
+  // p = wave and wave + 8) is rows 8 (p % 2) .. +7 of token fragment p / 2: lane l copies
+  // the 16-byte chunk c = (l % 8) ^ (l / 8) of row l / 8 of the K block, so each row's
+  // 128 bytes are read by 8 lanes (coalesced) and land in LDS with chunk c of fragment row
+  // q at 16 (c ^ (q % 8)) -- the swizzle keeps the fragment reads below free of bank
+  // conflicts.  Rows past M repeat row M - 1; their tokens are never stored.
+  const int arow = 8 * (wave & 1) + (lane >> 3);
+  const int achunk = (lane & 7) ^ (lane >> 3);
+  const uint8_t* xa0 = X + static_cast<size_t>(min(t0 + 16 * (wave >> 1) + arow, M - 1)) * K + achunk * 16;
+  const uint8_t* xa1 = X + static_cast<size_t>(min(t0 + 16 * (4 + (wave >> 1)) + arow, M - 1)) * K + achunk * 16;
+  const int srow = min(t0 + 64 * (wave & 1) + lane, M - 1);  // token scales (waves 0, 1)
   const int fr = lane < F - 1 ? lane : F - 1;
   const float* ws_src = Bs + static_cast<size_t>((16 * (F * tile + fr)) >> 7) * KB;  // weight scales (wave 2)
 
@@ -708,11 +713,19 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
       if (p < 2 * F)
         copy_to_lds16(B + packed_fragment(F * tile + (p >> 1), kb, NT) + (p & 1) * 1024 + lane * 16, st + p * 1024);
     }
-    const uint8_t* xk = X + static_cast<size_t>(kb) * MTT * 2048 + h * 1024 + lane * 16;
-    copy_to_lds16(xk + ta * 2048, st + Sh::W + wave * 1024);
-    copy_to_lds16(xk + tb * 2048, st + Sh::W + (8 + wave) * 1024);
-    if (wave < 2) copy_to_lds4(Xs + static_cast<size_t>(kb) * MTT * 16 + tok, st + Sh::TS + 256 * wave);
+    copy_to_lds16(xa0 + kb * 128, st + Sh::W + wave * 1024);
+    copy_to_lds16(xa1 + kb * 128, st + Sh::W + (8 + wave) * 1024);
+    if (wave < 2) copy_to_lds4(Xs + static_cast<size_t>(srow) * KB + kb, st + Sh::TS + 256 * wave);
     else if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
+  };
+  // MFMA operand of a token fragment in the swizzled layout: lane (r, g) reads chunks g
+  // and 4 + g of row r
+  const int ao0 = r * 128 + ((g ^ (r & 7)) << 4), ao1 = r * 128 + (((4 + g) ^ (r & 7)) << 4);
+  auto load_act = [&](const uint8_t* frag) {
+    const uint4 lo = *reinterpret_cast<const uint4*>(frag + ao0);
+    const uint4 hi = *reinterpret_cast<const uint4*>(frag + ao1);
+    return v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+               static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
   };
 
   v4f acc[FH][TJ];
@@ -732,7 +745,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     };
     auto load = [&](const uint8_t* st, Ops& o) {
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) o.a[j] = load_fragment(st + Sh::W + (TJ * tp + j) * 2048, lane);
+      for (int j = 0; j < TJ; ++j) o.a[j] = load_act(st + Sh::W + (TJ * tp + j) * 2048);
 #pragma unroll
       for (int f = 0; f < NR; ++f) o.w[f] = load_fragment(st + (f0 + f) * 2048, lane);
       const float* tsr = reinterpret_cast<const float*>(st + Sh::TS) + 16 * TJ * tp;
@@ -908,7 +921,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
     p.ksplit = 1;
     p.kb_per_split = KB;
     p.waves = kWideWaves;
-    p.xf = true;
+    p.xf = false;  // reads x [M, K] itself
     return p;
   }
   if (p.tiled) {
@@ -992,7 +1005,7 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
       constexpr int lds = WideShape<F_>::LDS;
       const void* fn = reinterpret_cast<const void*>(fp8_gemm_wide_kernel<F_>);
       if (const int rc = allow_dynamic_lds(fn, lds, "fp8_gemm")) return rc;
-      hipLaunchKernelGGL(fp8_gemm_wide_kernel<F_>, dim3(w.grid()), dim3(kWideWaves * 64), lds, st, xa, xsa, B, Bs, out,
+      hipLaunchKernelGGL(fp8_gemm_wide_kernel<F_>, dim3(w.grid()), dim3(kWideWaves * 64), lds, st, A, As, B, Bs, out,
                          part, cnt, M, N, K, w.TG, w.S, w.per);
       return check_launch("fp8_gemm");
     };
