@@ -83,10 +83,14 @@ GEMM_CASES = [
     (24, 6144, 512),    # 2 row tiles, 2 token tiles
     (48, 7168, 1024),   # 2 row tiles, 4 token tiles
     (64, 12288, 512),   # 4 row tiles, 4 token tiles
-    # M > 32, packed: wide MFMA GEMM
-    (65, 128, 512),     # one 8-row-tile slice split over all 4 K blocks: 4 partials
-    (192, 1024, 2048),  # 2 token groups, the second half full; 8 tiles x 16 K ranges
+    # M > 32, packed: wide MFMA GEMM (F row tiles per workgroup, S K ranges)
+    (65, 128, 512),     # F = 4: 2 slices, each split over all 4 K blocks: 4 partials
+    (192, 1024, 2048),  # F = 8: 2 token groups, the second half full; 8 tiles x 16 K ranges
     (40, 2048, 1024),   # one token group with 3 of its 8 fragments past M
+    (200, 640, 2048),   # F = 5
+    (200, 768, 2048),   # F = 6
+    (200, 1152, 2048),  # F = 9
+    (200, 4352, 1024),  # F = 8, K ranges of 3, 3 and 2 blocks
 ]
 
 
