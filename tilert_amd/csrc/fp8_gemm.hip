@@ -636,19 +636,21 @@ struct WideShape {
   static constexpr int FH = (F + 1) / 2;                // rows of the first split
   static constexpr int W = F * 2048;                    // weight fragments of one K block
   static constexpr int A = kWideTT * 2048;              // activation fragments
-  static constexpr int TS = W + A;                      // token scales (16 kWideTT floats)
-  static constexpr int WS = TS + kWideTT * 64;          // weight scales (F floats)
+  static constexpr int WS = W + A;                      // weight scales (F floats)
   static constexpr int STAGE = WS + 256;
-  static constexpr int LDS = kWideStages * STAGE;
+  static constexpr int WIN = kWideStages * STAGE;       // token-scale windows: [2][128][16] fp32
+  static constexpr int LDS = WIN + 2 * 128 * 16 * 4;
   static constexpr int SLOT = F * kWideTT * 256;        // floats of one partial
-  static_assert(kWideTT * 16 == 128, "two waves copy the token scales");
+  static_assert(kWideTT * 16 == 128, "8 waves x 16 tokens copy the token-scale windows");
 };
 
 // Copy instructions wave w issues per K block: its weight pieces (the 2F 1 KB pieces dealt
-// round robin), 2 activation pieces, and one scale copy for waves 0-1 (token scales) and
-// 2 (weight scales).
+// round robin), 2 activation pieces, and the weight scales (wave 2).  At the first block of
+// each 16-block window (and of the range) every wave also copies its 16 tokens' scales of
+// the window (4 more copies); those blocks' waits then cover a few copies of the next
+// block too, which is conservative.
 __host__ __device__ constexpr int wide_ops(int F, int w) {
-  return (2 * F - w + kWideWaves - 1) / kWideWaves + 2 + (w < 3 ? 1 : 0);
+  return (2 * F - w + kWideWaves - 1) / kWideWaves + 2 + (w == 2 ? 1 : 0);
 }
 
 // s_waitcnt needs an immediate: the wave-uniform count picks one of the possible waits
@@ -701,7 +703,12 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   const int achunk = (lane & 7) ^ (lane >> 3);
   const uint8_t* xa0 = X + static_cast<size_t>(min(t0 + 16 * (wave >> 1) + arow, M - 1)) * K + achunk * 16;
   const uint8_t* xa1 = X + static_cast<size_t>(min(t0 + 16 * (4 + (wave >> 1)) + arow, M - 1)) * K + achunk * 16;
-  const int srow = min(t0 + 64 * (wave & 1) + lane, M - 1);  // token scales (waves 0, 1)
+  // Token scales come in 16-block windows, double-buffered in LDS as [token][16] fp32:
+  // copy u of wave w brings tokens 16 w + 4 u .. +3 of the group, 16 lanes (64 contiguous
+  // bytes of x_s) per token; blocks past K repeat the row's last one.
+  const int srow[4] = {min(t0 + 16 * wave + (lane >> 4), M - 1), min(t0 + 16 * wave + 4 + (lane >> 4), M - 1),
+                       min(t0 + 16 * wave + 8 + (lane >> 4), M - 1), min(t0 + 16 * wave + 12 + (lane >> 4), M - 1)};
+  const int sblk = lane & 15;
   const int fr = lane < F - 1 ? lane : F - 1;
   const float* ws_src = Bs + static_cast<size_t>((16 * (F * tile + fr)) >> 7) * KB;  // weight scales (wave 2)
 
@@ -715,8 +722,13 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     }
     copy_to_lds16(xa0 + kb * 128, st + Sh::W + wave * 1024);
     copy_to_lds16(xa1 + kb * 128, st + Sh::W + (8 + wave) * 1024);
-    if (wave < 2) copy_to_lds4(Xs + static_cast<size_t>(srow) * KB + kb, st + Sh::TS + 256 * wave);
-    else if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
+    if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
+    if ((kb & 15) == 0 || kb == kb0) {  // the window of kb: a buffer last used 16 blocks ago
+      const int b = (kb & ~15) + sblk < KB ? (kb & ~15) + sblk : KB - 1;
+      uint8_t* win = smem + Sh::WIN + ((kb >> 4) & 1) * 8192 + wave * 1024;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) copy_to_lds4(Xs + static_cast<size_t>(srow[u]) * KB + b, win + u * 256);
+    }
   };
   // MFMA operand of a token fragment in the swizzled layout: lane (r, g) reads chunks g
   // and 4 + g of row r
@@ -743,15 +755,20 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
       v8i a[TJ], w[NR];
       float ts[TJ], ws[NR];
     };
-    auto load = [&](const uint8_t* st, Ops& o) {
+    auto stage = [&](int i) { return smem + (i & 3) * Sh::STAGE; };
+    auto last = [&](int i) { return kb0 + (i < n - 1 ? i : n - 1); };  // past the range: re-copy the last block
+    auto load = [&](int i, Ops& o) {  // block kb0 + i (past the range: unused values)
+      const uint8_t* st = stage(i);
+      const int kb = kb0 + i;
 #pragma unroll
       for (int j = 0; j < TJ; ++j) o.a[j] = load_act(st + Sh::W + (TJ * tp + j) * 2048);
 #pragma unroll
       for (int f = 0; f < NR; ++f) o.w[f] = load_fragment(st + (f0 + f) * 2048, lane);
-      const float* tsr = reinterpret_cast<const float*>(st + Sh::TS) + 16 * TJ * tp;
+      const float* tsr = reinterpret_cast<const float*>(smem + Sh::WIN + ((kb >> 4) & 1) * 8192) +
+                         (16 * TJ * tp + r) * 16 + (kb & 15);
       const float* wsr = reinterpret_cast<const float*>(st + Sh::WS) + f0;
 #pragma unroll
-      for (int j = 0; j < TJ; ++j) o.ts[j] = tsr[16 * j + r];
+      for (int j = 0; j < TJ; ++j) o.ts[j] = tsr[256 * j];
 #pragma unroll
       for (int f = 0; f < NR; ++f) o.ws[f] = wsr[f];
     };
@@ -768,8 +785,6 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[f][j] += pr[f][j] * (o.ts[j] * o.ws[f]);
     };
-    auto stage = [&](int i) { return smem + (i & 3) * Sh::STAGE; };
-    auto last = [&](int i) { return kb0 + (i < n - 1 ? i : n - 1); };  // past the range: re-copy the last block
     // Ring of 4 stages.  Iteration i: wait for block i + 1's copies (this wave's; the
     // barrier then covers every wave's), read them into the other register set, copy
     // block i + 3 into the stage block i - 1 used (its reads finished in iteration i - 2),
@@ -782,13 +797,13 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     wait_vm_ops(2 * ops);
     asm volatile("s_barrier" ::: "memory");
     Ops o0, o1;
-    load(stage(0), o0);
+    load(0, o0);
     auto step = [&](int i, const Ops& cur, Ops& nxt) {
       wait_vm_ops(ops);
       asm volatile("s_barrier" ::: "memory");
       issue(last(i + 3), stage(i + 3));
-      load(stage(i + 1), nxt);  // unconditional (past the range it reads a stage unused): no
-      mma(cur);                 // branch, so the wait for cur's reads stays partial
+      load(i + 1, nxt);  // unconditional (past the range it reads a stage unused): no
+      mma(cur);          // branch, so the wait for cur's reads stays partial
     };
     for (int i = 0; i < n; i += 2) {
       step(i, o0, o1);
