@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """MI355X benchmark of the FP8 decode hot path -- prints ONE JSON line.
 
-Headline (the BASELINE metric): the block-scaled FP8 linear 7168 -> 18432 at M = 4
+Headline (the workload's stated metric): the block-scaled FP8 linear 7168 -> 18432 at M = 4
 tokens (config 0's layer at decode + MTP=3 width): activations already quantised per
 1x128 (the rmsnorm_quant output the projection ops consume), weights e4m3fn with one
 fp32 scale per 128x128 block, output bf16.  One step = one GEMM call; K steps are

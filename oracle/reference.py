@@ -26,7 +26,7 @@ AMAX_FLOOR_F32 = torch.tensor(1e-4, dtype=torch.float32)
 
 SCALE_MODE_REFERENCE = 0  # s = amax * fp32(1/448)             refs/kernel.py:191
 SCALE_MODE_UE8M0 = 1  # s = 2^ceil(log2(amax * fp32(1/448)))  refs/kernel.py:140-151,189
-SCALE_MODE_DIV = 2  # s = amax / 448 (IEEE division), the BASELINE statement
+SCALE_MODE_DIV = 2  # s = amax / 448 (IEEE division), the workload's stated convention
 
 
 def _group_scale(amax: torch.Tensor, scale_mode: int) -> torch.Tensor:
@@ -94,7 +94,7 @@ def act_dequant(y: torch.Tensor, s: torch.Tensor, block_size: int = BLOCK) -> to
 def weight_quant(w: torch.Tensor, block_size: int = BLOCK) -> tuple[torch.Tensor, torch.Tensor]:
     """128x128 block quantisation of a weight (synthetic-weight preparation).
 
-    BASELINE convention: ``s = block_amax / 448`` (IEEE division), ``q = e4m3fn(w / s)``.
+    The workload's convention: ``s = block_amax / 448`` (IEEE division), ``q = e4m3fn(w / s)``.
     Rows/columns that do not fill a block (e.g. N=576) form a partial block.  All-zero
     blocks get s = 1 (so that dequantisation returns exact zeros).
     """
@@ -251,7 +251,7 @@ def indexer_scores(
     k: [L,128] e4m3fn with per-key scale [L]; w: bf16 [M,H]).  Token t sits at position
     ``cur_pos + t`` and sees keys ``l <= cur_pos + t``; masked positions are -inf.
     The reference ships no golden for this (ops/sparse_index.py:11-69 describes it as
-    "q * kv * weights"); the formula is the one BASELINE config 4 states.
+    "q * kv * weights"); the formula is the one the indexer workload (config 4) states.
     """
     M, H, Dh = q.shape
     L = k.shape[0]

@@ -170,7 +170,7 @@ def test_topk_accurate_reference_contract(cuda):
 
 
 def test_sparse_index_topk_128k(cuda):
-    """L = 131072, M = 4, 64 heads, top-2048, tokens at L-4..L-1."""
+    """Config 4 (the indexer workload): L = 131072, M = 4, 64 heads, top-2048, tokens at L-4..L-1."""
     M, H, L, k = 4, 64, 131072, 2048
     g = synth.gen(4)
     q, qs, kk, ks, w = synth.indexer_inputs(M, H, L, g)

@@ -4,7 +4,7 @@ into the layouts the kernels here run on -- the role of the reference's WeightCo
 (tilert/models/preprocess/weight_converter.py:243-403), which shards each layer's tensors
 per device before its per-op converters pack them.
 
-The share is the BASELINE layout: attention at tensor-parallel rank ``tp_rank`` of ``tp``
+The share is the plain TP / EP layout: attention at tensor-parallel rank ``tp_rank`` of ``tp``
 (q_b / kv_b rows and o_proj columns of ``n_heads / tp`` heads, q_a / kv_a replicated) and
 experts at expert-parallel rank ``ep_rank`` of ``ep`` (experts ``n_experts / ep * ep_rank``
 onwards, whole).  (The reference instead shards each expert's inter dim across devices,
@@ -145,8 +145,8 @@ def load_expert_shard(ckpt: Checkpoint, layer: int, ep_rank: int, ep: int, devic
 
 
 def load_dense_mlp(ckpt: Checkpoint, layer: int, device: torch.device) -> dict[str, PackedFP8Weight]:
-    """The dense MLP of ``model.layers.{layer}`` (gate / up / down, unsharded: BASELINE
-    config 3's 7168 <-> 18432 layers), packed."""
+    """The dense MLP of ``model.layers.{layer}`` (gate / up / down, unsharded: the
+    7168 <-> 18432 layers of the dense-MLP workload), packed."""
     out = {}
     for k in ("gate_proj", "up_proj", "down_proj"):
         w, s = ckpt.fp8(f"model.layers.{layer}.mlp.{k}")

@@ -65,7 +65,8 @@ __device__ inline uint32_t f32_to_e4m3(float v) {
 
 // Quantisation scale of a 128-element group from its fp32 amax; mirrors
 // refs/kernel.py:186-191 (amax floor 1e-4, s = amax * fp32(1/448)) and the power-of-two
-// round-scale form :140-151; TL_SCALE_DIV is BASELINE's amax / 448.
+// round-scale form :140-151; TL_SCALE_DIV is the plain amax / 448 (IEEE division) of the
+// workload's statement.
 __device__ inline float group_scale(float amax, int scale_mode) {
   amax = fmaxf(amax, 1e-4f);
   if (scale_mode == TL_SCALE_UE8M0) {

@@ -1,5 +1,5 @@
-"""MoE expert layer at one expert-parallel shard (32 local experts of
-256, whole experts per GPU), on the gfx950 HIP kernels:
+"""MoE expert layer at one expert-parallel shard (EP = 8: 32 local experts of 256, whole
+experts per GPU), on the gfx950 HIP kernels:
   * ``ep_gate_up_swiglu``: grouped gate/up GEMM + SwiGLU for the shard's hit experts (the
     grouped GEMM of expert_select_up_gate_silu_op, deepseek_v3_2/ops/
     expert_sel_up_gate_silu.py:23-48, golden :670-692);

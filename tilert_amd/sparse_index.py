@@ -118,7 +118,8 @@ def ki_pages_from_flat(kv: torch.Tensor, k_scale: torch.Tensor) -> torch.Tensor:
 def ki_cache_write(keys: torch.Tensor, ki_pages: torch.Tensor, pos: int, scale_fmt: str | None = "div") -> None:
     """Quantise ``keys`` (bf16 [n, 128]) per key to e4m3fn with an fp32 scale and store them
     at positions pos .. pos+n-1 of ``ki_pages`` (uint8 [n_pages, 8448]).  ``scale_fmt`` as in
-    ``act_quant``; the default "div" is BASELINE's per-token amax / 448."""
+    ``act_quant``; the default "div" is the per-token amax / 448 of the
+    workload's key cache."""
     if keys.dtype != torch.bfloat16 or keys.dim() != 2 or keys.shape[1] != 128 or not keys.is_contiguous():
         raise ValueError("keys must be a contiguous bfloat16 [n, 128] tensor")
     if ki_pages.dtype != torch.uint8 or ki_pages.dim() != 2 or ki_pages.shape[1] != KI_PAGE_BYTES \
