@@ -91,6 +91,8 @@ GEMM_CASES = [
     (200, 768, 2048),   # F = 6
     (200, 1152, 2048),  # F = 9
     (200, 4352, 1024),  # F = 8, K ranges of 3, 3 and 2 blocks
+    (255, 2048, 1024),  # last token fragment 15/16 full, second token group
+    (33, 7168, 512),    # 3 of 8 token fragments valid, 4 K ranges of one block
 ]
 
 
