@@ -90,7 +90,7 @@ int tl_weight_dequant(const void* q_fp8, const float* s, void* out, int out_bf16
  * a fp8 [M,K], a_s fp32 [M,K/128], b fp8 [N,K], b_s fp32 [ceil(N/128),K/128].
  * Requires K % 128 == 0, N % 16 == 0, 1 <= M <= 256, 16-byte aligned a and b.
  * From M = 16 on (a rearranged copy of the activations, or the packed MFMA GEMM's split-K
- * partials from M = 33) and for narrow layers at M > 16 (split-K partials) the call needs
+ * partials from M = 17 or 33) and for narrow layers at M > 16 (split-K partials) the call needs
  * a workspace of tl_fp8_gemm_workspace_bytes(M,N,K)
  * bytes (0 = none), ZERO-FILLED before its first use; the kernels leave it ready for the
  * next call.  Calls that share a workspace must be ordered
@@ -114,7 +114,7 @@ int tl_fp8_pack_weight(const void* b, void* packed, int64_t N, int64_t K, void* 
 
 /* tl_fp8_gemm with b in the fragment-packed layout of tl_fp8_pack_weight (same scales,
  * same workspace rule).  Results equal tl_fp8_gemm's bit for bit where both run the GEMV
- * (M <= 32, or N % 128 != 0); from M = 33 with N % 128 == 0 the packed layout runs an MFMA
+ * (M <= 16, or N % 128 != 0); from M = 17 or 33 with N % 128 == 0 the packed layout runs an MFMA
  * GEMM that sums the K blocks in another order (same tolerance against the reference).
  * The FP8 GEMV / GEMM behind the reference's packed-weight projection ops (projx_wqkva_op,
  * rmsnorm_up_gate_silu_op, ...). */

@@ -52,7 +52,7 @@ class _Layer:
         assert_gemm_close(out_c, want, "canonical " + what)
         assert_gemm_close(out_p, want, "packed " + what)
         assert torch.equal(out_p, out_p2), "packed GEMM not deterministic: " + what
-        if M <= 32:  # the same GEMV on both layouts
+        if M <= 16:  # the same GEMV on both layouts
             assert torch.equal(out_c, out_p), "layouts differ: " + what
 
 

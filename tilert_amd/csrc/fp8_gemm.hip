@@ -17,15 +17,17 @@
 //     each wave-wide load reads 1 KB of consecutive memory.  Packing is done once at
 //     weight-load time (tl_fp8_pack_weight), like the reference's per-op weight
 //     converters.  Measured on MI355X: packed fragments stream ~25% faster.
-//   * M <= 64 (fp8_gemm_kernel; M <= 32 on packed weights with N % 128 = 0): a workgroup
+//   * M <= 64 (fp8_gemm_kernel; on packed weights with N % 128 = 0 only up to M = 16, and
+//     at M = 17..32 where the wide kernel below would split K in more than 2): a workgroup
 //     owns one 16-row tile and a slice of K blocks;
 //     its 4-8 waves interleave over the slice, each with the next block's operands in
 //     flight (two buffers in ping-pong; deeper rings measured no faster), and are summed
 //     through LDS in a fixed order.  The K split is chosen so the grid covers the 256 CUs
 //     evenly; the last workgroup of a row tile (agent-scope counter and agent-scope atomic
 //     partials) sums the fp32 partials in slice order, so results are deterministic.
-//   * M > 32 on packed weights with N % 128 = 0 (fp8_gemm_wide_kernel): F row tiles x 128
-//     tokens per workgroup, one balanced round of 256 workgroups, operands staged in LDS.
+//   * from M = 17 or 33 on packed weights with N % 128 = 0 (fp8_gemm_wide_kernel): F row
+//     tiles x 64 or 128 tokens per workgroup, one balanced round of 256 workgroups,
+//     operands staged in LDS.
 //   * M > 64 otherwise (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks
 //     staged in LDS (see below).
 #include <algorithm>
@@ -593,14 +595,15 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 }
 
 // ---------------------------------------------------------------- M > 32: MFMA GEMM
-// Wide-tile MFMA GEMM for 32 < M <= 256 on packed weights (fp8_gemm_wide_kernel<F>).
+// Wide-tile MFMA GEMM for 16 < M <= 256 on packed weights (fp8_gemm_wide_kernel<F, TJ>).
 // A workgroup (8 waves, one workgroup per CU) owns F consecutive 16-row weight tiles x one
-// group of 8 token fragments (128 tokens) over one of S K ranges.  The host picks F (4..9)
-// and S so that tiles x token groups x S <= 256 workgroups give every CU the same work in
-// one round (up 7168 -> 18432 at M = 256: F = 9, 128 row tiles x 2 token groups; down
-// 18432 -> 7168: F = 7, 64 x 2 x 2 K ranges).  Waves w and w + 4 (one SIMD) share token
-// pair w % 4 and split the F rows, so every fragment a wave reads from LDS feeds 2 or 5
-// MFMAs and each SIMD has two waves to hide the other's latencies.
+// group of 4 TJ token fragments (64 or 128 tokens; TJ = 1 up to M = 64) over one of S K
+// ranges.  The host picks F (4..9) and S so that tiles x token groups x S <= 256
+// workgroups give every CU the same work in one round (up 7168 -> 18432 at M = 256: F = 9,
+// 128 row tiles x 2 token groups; down 18432 -> 7168: F = 7, 64 x 2 x 2 K ranges).  Waves
+// w and w + 4 (one SIMD) share token fragments w % 4 and split the F rows, so every
+// fragment a wave reads from LDS feeds several MFMAs and each SIMD has two waves to hide
+// the other's latencies.
 // Per K block the weight fragments, the activation rows (read from x [M, K] itself) and
 // their scales are copied global -> LDS (global_load_lds, no registers) into a 4-stage
 // ring; each wave reads block i + 1's operands into a second register set while
@@ -617,13 +620,14 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 // workgroup that completes a tile (agent-scope counter) sums them in range order, so
 // results are deterministic.
 constexpr int kWideStages = 4;
-// From M = 33 on the wide kernel beats the GEMV on packed weights (measured: up 7168 ->
-// 18432 at M = 33 / 48 / 64: 37.9 / 38.8 / 38.9 vs 48.9 / 49.1 / 51.2 us; down 18432 ->
-// 7168 level at ~40 us); at M = 17 the GEMV is faster (35.7 vs 37.4 us).
-constexpr int kWideMinM = 32;
+// When the wide kernel replaces the GEMV on packed weights (measured, us, wide vs GEMV):
+// from M = 33 on always (up 7168 -> 18432 at M = 33 / 48 / 64: 28.1 / 28.7 / 29.5 vs
+// 48.9 / 49.1 / 51.2; down 18432 -> 7168 at M = 64: 37.5 vs 41.3); at M = 17..32 only when
+// its plan splits K at most in 2 (up at M = 17 / 32: 28.5 / 27.9 vs 35.7 / 35.8; down,
+// split in 4: 37.2 / 37.5 vs 30.2 / 30.3); at M <= 16 never (up at M = 16: GEMV 27.2).
+constexpr int kWideMinM = 32;   // from M = 33 on always
+constexpr int kWideMinM2 = 16;  // from M = 17 on when at most 2 K ranges
 constexpr int kWideGrid = 256;
-constexpr int kWideTJ = 2;              // token fragments per wave
-constexpr int kWideTT = 4 * kWideTJ;    // token fragments per workgroup (4 token pairs)
 constexpr int kCpolSc1 = 16;            // buffer access cache policy: sc1
 constexpr int kRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
 
@@ -631,26 +635,29 @@ constexpr int kRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data f
 // (FH and F - FH), so each SIMD has two waves to hide the other's LDS and MFMA latencies.
 constexpr int kWideWaves = 8;
 
-template <int F>
+// TJ: token fragments per wave (1 up to M = 64, else 2); a workgroup covers TT = 4 TJ
+// token fragments (16 TT tokens).
+template <int F, int TJ>
 struct WideShape {
+  static constexpr int TT = 4 * TJ;
   static constexpr int FH = (F + 1) / 2;                // rows of the first split
   static constexpr int W = F * 2048;                    // weight fragments of one K block
-  static constexpr int A = kWideTT * 2048;              // activation fragments
+  static constexpr int A = TT * 2048;                   // activation fragments
   static constexpr int WS = W + A;                      // weight scales (F floats)
   static constexpr int STAGE = WS + 256;
   static constexpr int WIN = kWideStages * STAGE;       // token-scale windows: [2][128][16] fp32
   static constexpr int LDS = WIN + 2 * 128 * 16 * 4;
-  static constexpr int SLOT = F * kWideTT * 256;        // floats of one partial
-  static_assert(kWideTT * 16 == 128, "8 waves x 16 tokens copy the token-scale windows");
+  static constexpr int SLOT = F * TT * 256;             // floats of one partial
+  static_assert(16 * TT <= 128, "the token-scale windows hold 128 tokens");
 };
 
 // Copy instructions wave w issues per K block: its weight pieces (the 2F 1 KB pieces dealt
-// round robin), 2 activation pieces, and the weight scales (wave 2).  At the first block of
-// each 16-block window (and of the range) every wave also copies its 16 tokens' scales of
-// the window (4 more copies); those blocks' waits then cover a few copies of the next
-// block too, which is conservative.
-__host__ __device__ constexpr int wide_ops(int F, int w) {
-  return (2 * F - w + kWideWaves - 1) / kWideWaves + 2 + (w == 2 ? 1 : 0);
+// round robin), TJ activation pieces, and the weight scales (wave 2).  At the first block
+// of each 16-block window (and of the range) waves 0 .. TT - 1 also copy their 16 tokens'
+// scales of the window (4 more copies); those blocks' waits then cover a few copies of the
+// next block too, which is conservative.
+__host__ __device__ constexpr int wide_ops(int F, int TJ, int w) {
+  return (2 * F - w + kWideWaves - 1) / kWideWaves + TJ + (w == 2 ? 1 : 0);
 }
 
 // s_waitcnt needs an immediate: the wave-uniform count picks one of the possible waits
@@ -667,14 +674,14 @@ __device__ inline void wait_vm_ops(int ops) {
   }
 }
 
-template <int F>
+template <int F, int TJ>
 __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int TG, int S, int per) {
   // X [M, K] e4m3fn and Xs [M, K / 128] fp32: the activations and their scales
-  using Sh = WideShape<F>;
-  constexpr int TJ = kWideTJ, TT = kWideTT, FH = Sh::FH;
+  using Sh = WideShape<F, TJ>;
+  constexpr int TT = Sh::TT, FH = Sh::FH;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ uint32_t last_flag;
   const int KB = K >> 7, NT = N >> 4;
@@ -692,17 +699,19 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   const int t0 = 16 * TT * tg;        // first token of the group
   const int tf0 = TT * tg + TJ * tp;  // this wave's first token fragment
   const int f0 = rh * FH;             // this wave's first row fragment
-  const int ops = wide_ops(F, wave);
-  // Activations straight from x [M, K] (no image pass).  Piece p of the group (waves copy
-  // p = wave and wave + 8) is rows 8 (p % 2) .. +7 of token fragment p / 2: lane l copies
+  const int ops = wide_ops(F, TJ, wave);
+  // Activations straight from x [M, K] (no image pass).  Piece p of the group (wave w copies
+  // p = w + 8 u, u < TJ) is rows 8 (p % 2) .. +7 of token fragment p / 2: lane l copies
   // the 16-byte chunk c = (l % 8) ^ (l / 8) of row l / 8 of the K block, so each row's
   // 128 bytes are read by 8 lanes (coalesced) and land in LDS with chunk c of fragment row
   // q at 16 (c ^ (q % 8)) -- the swizzle keeps the fragment reads below free of bank
   // conflicts.  Rows past M repeat row M - 1; their tokens are never stored.
   const int arow = 8 * (wave & 1) + (lane >> 3);
   const int achunk = (lane & 7) ^ (lane >> 3);
-  const uint8_t* xa0 = X + static_cast<size_t>(min(t0 + 16 * (wave >> 1) + arow, M - 1)) * K + achunk * 16;
-  const uint8_t* xa1 = X + static_cast<size_t>(min(t0 + 16 * (4 + (wave >> 1)) + arow, M - 1)) * K + achunk * 16;
+  const uint8_t* xa[TJ];
+#pragma unroll
+  for (int u = 0; u < TJ; ++u)
+    xa[u] = X + static_cast<size_t>(min(t0 + 16 * (4 * u + (wave >> 1)) + arow, M - 1)) * K + achunk * 16;
   // Token scales come in 16-block windows, double-buffered in LDS as [token][16] fp32:
   // copy u of wave w brings tokens 16 w + 4 u .. +3 of the group, 16 lanes (64 contiguous
   // bytes of x_s) per token; blocks past K repeat the row's last one.
@@ -720,10 +729,10 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
       if (p < 2 * F)
         copy_to_lds16(B + packed_fragment(F * tile + (p >> 1), kb, NT) + (p & 1) * 1024 + lane * 16, st + p * 1024);
     }
-    copy_to_lds16(xa0 + kb * 128, st + Sh::W + wave * 1024);
-    copy_to_lds16(xa1 + kb * 128, st + Sh::W + (8 + wave) * 1024);
+#pragma unroll
+    for (int u = 0; u < TJ; ++u) copy_to_lds16(xa[u] + kb * 128, st + Sh::W + (wave + 8 * u) * 1024);
     if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
-    if ((kb & 15) == 0 || kb == kb0) {  // the window of kb: a buffer last used 16 blocks ago
+    if (wave < TT && ((kb & 15) == 0 || kb == kb0)) {  // the window of kb: a buffer last used 16 blocks ago
       const int b = (kb & ~15) + sblk < KB ? (kb & ~15) + sblk : KB - 1;
       uint8_t* win = smem + Sh::WIN + ((kb >> 4) & 1) * 8192 + wave * 1024;
 #pragma unroll
@@ -874,14 +883,15 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
 // -- with at most 256 workgroups per round (token groups x tiles x S); ties go to fewer
 // K ranges.  F = 0: no F divides N / 16.
 struct WidePlan {
-  int F, TG, S, per, tiles;
+  int F, TJ, TG, S, per, tiles;
   int grid() const { return static_cast<int>(cdiv(static_cast<int64_t>(tiles) * S, 8)) * 8 * TG; }
 };
 
 __host__ inline WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
   const int NT = static_cast<int>(N / 16), KB = static_cast<int>(K / kBlock);
-  const int TG = static_cast<int>(cdiv(cdiv(M, 16), kWideTT));
-  WidePlan best{0, TG, 1, KB, 0};
+  const int TJ = cdiv(M, 16) <= 4 ? 1 : 2;
+  const int TG = static_cast<int>(cdiv(cdiv(M, 16), 4 * TJ));
+  WidePlan best{0, TJ, TG, 1, KB, 0};
   int64_t best_cost = INT64_MAX;
   for (int F = 9; F >= 4; --F) {
     if (NT % F) continue;
@@ -890,7 +900,7 @@ __host__ inline WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
     const int per = static_cast<int>(cdiv(KB, S));
     S = static_cast<int>(cdiv(KB, per));
     const int64_t cost = cdiv(static_cast<int64_t>(tiles) * TG * S, kWideGrid) * F * per * 16 + (S - 1);
-    if (cost < best_cost) { best_cost = cost; best = WidePlan{F, TG, S, per, tiles}; }
+    if (cost < best_cost) { best_cost = cost; best = WidePlan{F, TJ, TG, S, per, tiles}; }
   }
   return best;
 }
@@ -898,12 +908,12 @@ __host__ inline WidePlan plan_wide(int64_t M, int64_t N, int64_t K) {
 __host__ inline size_t wide_partial_bytes(int64_t M, int64_t N, int64_t K) {
   const WidePlan w = plan_wide(M, N, K);
   if (w.S == 1) return 0;
-  return static_cast<size_t>(w.tiles) * w.TG * w.S * w.F * kWideTT * 256 * sizeof(float);
+  return static_cast<size_t>(w.tiles) * w.TG * w.S * w.F * 4 * w.TJ * 256 * sizeof(float);
 }
 
 
 struct GemmPlan {
-  bool mm;     // M > 32, packed weight, N % 128 = 0: fp8_gemm_wide_kernel
+  bool mm;     // packed weight, N % 128 = 0, M > 32 (or > 16, K split <= 2): fp8_gemm_wide_kernel
   bool tiled;  // M > 64, canonical weight: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
@@ -926,7 +936,8 @@ struct GemmPlan {
 static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
-  p.mm = M > kWideMinM && packed && N % 128 == 0 && K % (kBlock * kGroup) == 0;
+  p.mm = packed && N % 128 == 0 && K % (kBlock * kGroup) == 0 &&
+         (M > kWideMinM || (M > kWideMinM2 && plan_wide(M, N, K).S <= 2));
   p.tiled = M > 64 && !p.mm;
   p.depth = 2;
   p.rt = 1;
@@ -1015,23 +1026,27 @@ static int launch_gemm(const uint8_t* A, const float* As, const uint8_t* B, cons
     uint32_t* cnt = static_cast<uint32_t*>(workspace);
     float* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     const WidePlan w = plan_wide(M, N, K);
-    auto go = [&](auto f_tag) -> int {
-      constexpr int F_ = decltype(f_tag)::value;
-      constexpr int lds = WideShape<F_>::LDS;
-      const void* fn = reinterpret_cast<const void*>(fp8_gemm_wide_kernel<F_>);
+    auto go = [&](auto f_tag, auto tj_tag) -> int {
+      constexpr int F_ = decltype(f_tag)::value, TJ_ = decltype(tj_tag)::value;
+      constexpr int lds = WideShape<F_, TJ_>::LDS;
+      const void* fn = reinterpret_cast<const void*>(fp8_gemm_wide_kernel<F_, TJ_>);
       if (const int rc = allow_dynamic_lds(fn, lds, "fp8_gemm")) return rc;
-      hipLaunchKernelGGL(fp8_gemm_wide_kernel<F_>, dim3(w.grid()), dim3(kWideWaves * 64), lds, st, A, As, B, Bs, out,
-                         part, cnt, M, N, K, w.TG, w.S, w.per);
+      hipLaunchKernelGGL((fp8_gemm_wide_kernel<F_, TJ_>), dim3(w.grid()), dim3(kWideWaves * 64), lds, st, A, As, B,
+                         Bs, out, part, cnt, M, N, K, w.TG, w.S, w.per);
       return check_launch("fp8_gemm");
     };
-    switch (w.F) {
-      case 9: return go(std::integral_constant<int, 9>{});
-      case 8: return go(std::integral_constant<int, 8>{});
-      case 7: return go(std::integral_constant<int, 7>{});
-      case 6: return go(std::integral_constant<int, 6>{});
-      case 5: return go(std::integral_constant<int, 5>{});
-      default: return go(std::integral_constant<int, 4>{});
-    }
+    auto go_f = [&](auto tj_tag) -> int {
+      switch (w.F) {
+        case 9: return go(std::integral_constant<int, 9>{}, tj_tag);
+        case 8: return go(std::integral_constant<int, 8>{}, tj_tag);
+        case 7: return go(std::integral_constant<int, 7>{}, tj_tag);
+        case 6: return go(std::integral_constant<int, 6>{}, tj_tag);
+        case 5: return go(std::integral_constant<int, 5>{}, tj_tag);
+        default: return go(std::integral_constant<int, 4>{}, tj_tag);
+      }
+    };
+    if (w.TJ == 1) return go_f(std::integral_constant<int, 1>{});
+    return go_f(std::integral_constant<int, 2>{});
   }
   if (p.tiled) {
     auto launch = [&](auto tt_tag) -> int {
