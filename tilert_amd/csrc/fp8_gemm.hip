@@ -18,14 +18,15 @@
 //     weight-load time (tl_fp8_pack_weight), like the reference's per-op weight
 //     converters.  Measured on MI355X: packed fragments stream ~25% faster.
 //   * M <= 64 (fp8_gemm_kernel; on packed weights with N % 128 = 0 only up to M = 16, and
-//     at M = 17..32 where the wide kernel below would split K in more than 2): a workgroup
+//     at M = 17..32 where the wide kernel below would split K in more than 4): a workgroup
 //     owns one 16-row tile and a slice of K blocks;
 //     its 4-8 waves interleave over the slice, each with the next block's operands in
 //     flight (two buffers in ping-pong; deeper rings measured no faster), and are summed
 //     through LDS in a fixed order.  The K split is chosen so the grid covers the 256 CUs
 //     evenly; the last workgroup of a row tile (agent-scope counter and agent-scope atomic
 //     partials) sums the fp32 partials in slice order, so results are deterministic.
-//   * from M = 17 or 33 on packed weights with N % 128 = 0 (fp8_gemm_wide_kernel): F row
+//   * from M = 17 (K split in <= 4) or 33 on packed weights with N % 128 = 0
+//     (fp8_gemm_wide_kernel): F row
 //     tiles x 64 or 128 tokens per workgroup, one balanced round of 256 workgroups,
 //     operands staged in LDS.
 //   * M > 64 otherwise (fp8_gemm_tiled_kernel): 128-row workgroups share activation chunks
@@ -619,14 +620,16 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 // read with 16-byte sc1 accesses (past this XCD's L2, like agent-scope atomics); the
 // workgroup that completes a tile (agent-scope counter) sums them in range order, so
 // results are deterministic.
-constexpr int kWideStages = 4;
 // When the wide kernel replaces the GEMV on packed weights (measured, us, wide vs GEMV):
 // from M = 33 on always (up 7168 -> 18432 at M = 33 / 48 / 64: 28.1 / 28.7 / 29.5 vs
-// 48.9 / 49.1 / 51.2; down 18432 -> 7168 at M = 64: 37.5 vs 41.3); at M = 17..32 only when
-// its plan splits K at most in 2 (up at M = 17 / 32: 28.5 / 27.9 vs 35.7 / 35.8; down,
-// split in 4: 37.2 / 37.5 vs 30.2 / 30.3); at M <= 16 never (up at M = 16: GEMV 27.2).
-constexpr int kWideMinM = 32;   // from M = 33 on always
-constexpr int kWideMinM2 = 16;  // from M = 17 on when at most 2 K ranges
+// 48.9 / 49.1 / 51.2; down 18432 -> 7168 at M = 64: 29.8 vs 41.3; 7168 -> 1536 at M = 64:
+// 12.7 vs 22.5); at M = 17..32 only when its plan splits K at most in 4 (up at M = 17 / 32:
+// 28.5 / 27.9 vs 35.7 / 35.8; down at M = 17 / 24 / 32: 29.4 / 29.1 / 29.4 vs 30.2 / 30.3 /
+// 30.3; small layers that split K 8 ways or more lose: 7168 -> 1024 at M = 32 14.3 vs
+// 10.5, 2048 -> 4096 at M = 24 9.5 vs 6.5); at M <= 16 never (up at M = 16: GEMV 27.2).
+constexpr int kWideMinM = 32;      // from M = 33 on always
+constexpr int kWideMinM2 = 16;     // from M = 17 on when the K split is small:
+constexpr int kWideMaxSplit2 = 4;  // at most this many K ranges
 constexpr int kWideGrid = 256;
 constexpr int kCpolSc1 = 16;            // buffer access cache policy: sc1
 constexpr int kRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
@@ -640,12 +643,13 @@ constexpr int kWideWaves = 8;
 template <int F, int TJ>
 struct WideShape {
   static constexpr int TT = 4 * TJ;
+  static constexpr int STAGES = 4;                      // ring depth (5 measured no faster at TJ = 1)
   static constexpr int FH = (F + 1) / 2;                // rows of the first split
   static constexpr int W = F * 2048;                    // weight fragments of one K block
   static constexpr int A = TT * 2048;                   // activation fragments
   static constexpr int WS = W + A;                      // weight scales (F floats)
   static constexpr int STAGE = WS + 256;
-  static constexpr int WIN = kWideStages * STAGE;       // token-scale windows: [2][128][16] fp32
+  static constexpr int WIN = STAGES * STAGE;            // token-scale windows: [2][128][16] fp32
   static constexpr int LDS = WIN + 2 * 128 * 16 * 4;
   static constexpr int SLOT = F * TT * 256;             // floats of one partial
   static_assert(16 * TT <= 128, "the token-scale windows hold 128 tokens");
@@ -661,15 +665,16 @@ __host__ __device__ constexpr int wide_ops(int F, int TJ, int w) {
 }
 
 // s_waitcnt needs an immediate: the wave-uniform count picks one of the possible waits
+// (every count a ring of these kernels can need, 1..24; larger ones wait for everything)
 __device__ inline void wait_vm_ops(int ops) {
   switch (ops) {
-    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_imm(3)); break;
-    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4)); break;
-    case 5: __builtin_amdgcn_s_waitcnt(vmcnt_imm(5)); break;
-    case 6: __builtin_amdgcn_s_waitcnt(vmcnt_imm(6)); break;
-    case 8: __builtin_amdgcn_s_waitcnt(vmcnt_imm(8)); break;
-    case 10: __builtin_amdgcn_s_waitcnt(vmcnt_imm(10)); break;
-    case 12: __builtin_amdgcn_s_waitcnt(vmcnt_imm(12)); break;
+#define TL_WAIT_CASE(n) \
+  case n: __builtin_amdgcn_s_waitcnt(vmcnt_imm(n)); break;
+    TL_WAIT_CASE(1) TL_WAIT_CASE(2) TL_WAIT_CASE(3) TL_WAIT_CASE(4) TL_WAIT_CASE(5) TL_WAIT_CASE(6)
+    TL_WAIT_CASE(7) TL_WAIT_CASE(8) TL_WAIT_CASE(9) TL_WAIT_CASE(10) TL_WAIT_CASE(11) TL_WAIT_CASE(12)
+    TL_WAIT_CASE(13) TL_WAIT_CASE(14) TL_WAIT_CASE(15) TL_WAIT_CASE(16) TL_WAIT_CASE(17) TL_WAIT_CASE(18)
+    TL_WAIT_CASE(19) TL_WAIT_CASE(20) TL_WAIT_CASE(21) TL_WAIT_CASE(22) TL_WAIT_CASE(23) TL_WAIT_CASE(24)
+#undef TL_WAIT_CASE
     default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
   }
 }
@@ -764,7 +769,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
       v8i a[TJ], w[NR];
       float ts[TJ], ws[NR];
     };
-    auto stage = [&](int i) { return smem + (i & 3) * Sh::STAGE; };
+    auto stage = [&](int i) { return smem + (i % Sh::STAGES) * Sh::STAGE; };
     auto last = [&](int i) { return kb0 + (i < n - 1 ? i : n - 1); };  // past the range: re-copy the last block
     auto load = [&](int i, Ops& o) {  // block kb0 + i (past the range: unused values)
       const uint8_t* st = stage(i);
@@ -794,23 +799,21 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
 #pragma unroll
         for (int j = 0; j < TJ; ++j) acc[f][j] += pr[f][j] * (o.ts[j] * o.ws[f]);
     };
-    // Ring of 4 stages.  Iteration i: wait for block i + 1's copies (this wave's; the
+    // Ring of SN stages.  Iteration i: wait for block i + 1's copies (this wave's; the
     // barrier then covers every wave's), read them into the other register set, copy
-    // block i + 3 into the stage block i - 1 used (its reads finished in iteration i - 2),
-    // and multiply block i.  Each wave always has the same number of its copies in
+    // block i + SN - 1 into the stage block i - 1 used (its reads finished in iteration
+    // i - 2), and multiply block i.  Each wave always has the same number of its copies in
     // flight, so the wait counts are fixed.
-    static_assert(kWideStages == 4, "wait counts below assume 4 stages");
-    issue(last(0), stage(0));
-    issue(last(1), stage(1));
-    issue(last(2), stage(2));
-    wait_vm_ops(2 * ops);
+    constexpr int SN = Sh::STAGES;
+    static_for<SN - 1>([&](auto j) { issue(last(decltype(j)::value), stage(decltype(j)::value)); });
+    wait_vm_ops((SN - 2) * ops);  // block 0 landed
     asm volatile("s_barrier" ::: "memory");
     Ops o0, o1;
     load(0, o0);
     auto step = [&](int i, const Ops& cur, Ops& nxt) {
-      wait_vm_ops(ops);
+      wait_vm_ops((SN - 3) * ops);  // block i + 1 landed (blocks i + 2 .. i + SN - 2 may not have)
       asm volatile("s_barrier" ::: "memory");
-      issue(last(i + 3), stage(i + 3));
+      issue(last(i + SN - 1), stage(i + SN - 1));
       load(i + 1, nxt);  // unconditional (past the range it reads a stage unused): no
       mma(cur);          // branch, so the wait for cur's reads stays partial
     };
@@ -913,7 +916,7 @@ __host__ inline size_t wide_partial_bytes(int64_t M, int64_t N, int64_t K) {
 
 
 struct GemmPlan {
-  bool mm;     // packed weight, N % 128 = 0, M > 32 (or > 16, K split <= 2): fp8_gemm_wide_kernel
+  bool mm;     // packed weight, N % 128 = 0, M > 32 (or > 16, K split <= 4): fp8_gemm_wide_kernel
   bool tiled;  // M > 64, canonical weight: fp8_gemm_tiled_kernel
   int ksplit;
   int kb_per_split;
@@ -937,7 +940,7 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
   GemmPlan p;
   const int KB = static_cast<int>(K / kBlock);
   p.mm = packed && N % 128 == 0 && K % (kBlock * kGroup) == 0 &&
-         (M > kWideMinM || (M > kWideMinM2 && plan_wide(M, N, K).S <= 2));
+         (M > kWideMinM || (M > kWideMinM2 && plan_wide(M, N, K).S <= kWideMaxSplit2));
   p.tiled = M > 64 && !p.mm;
   p.depth = 2;
   p.rt = 1;
