@@ -679,6 +679,21 @@ __device__ inline void wait_vm_ops(int ops) {
   }
 }
 
+// Load-to-LDS copies as in copy_to_lds16 / copy_to_lds4 (common.h), but taking the LDS
+// address as a wave-uniform 32-bit value already computed, with no generic-to-LDS pointer
+// conversion per copy (m0, a reserved register, is saved and restored as there): the wide
+// kernel issues 4-8 of these per K block.
+__device__ inline void dma_lds16(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+__device__ inline void dma_lds4(const void* src, uint32_t lds) {
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+}
+
 template <int F, int TJ>
 __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     const uint8_t* __restrict__ X, const float* __restrict__ Xs, const uint8_t* __restrict__ B,
@@ -726,22 +741,34 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   const int fr = lane < F - 1 ? lane : F - 1;
   const float* ws_src = Bs + static_cast<size_t>((16 * (F * tile + fr)) >> 7) * KB;  // weight scales (wave 2)
 
-  // copies of K block kb into stage st
-  auto issue = [&](int kb, uint8_t* st) {
+  // this lane's weight pieces at K block 0 (a block's fragments lie a fixed offset further)
+  constexpr int WPW = (2 * F + kWideWaves - 1) / kWideWaves;
+  const uint8_t* wsrc[WPW];
 #pragma unroll
-    for (int u = 0; u < (2 * F + kWideWaves - 1) / kWideWaves; ++u) {
+  for (int u = 0; u < WPW; ++u) {
+    const int p = wave + kWideWaves * u < 2 * F - 1 ? wave + kWideWaves * u : 2 * F - 1;
+    wsrc[u] = B + packed_fragment(F * tile + (p >> 1), 0, NT) + (p & 1) * 1024 + lane * 16;
+  }
+  const uint32_t lds0 =
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_u8_ptr)smem)));
+
+  // copies of K block kb into stage sidx
+  auto issue = [&](int kb, int sidx) {
+    const uint32_t ls = lds0 + sidx * Sh::STAGE;
+    const size_t koff = (static_cast<size_t>(kb >> 2) * NT * kGroup + (kb & 3)) * 2048;
+#pragma unroll
+    for (int u = 0; u < WPW; ++u) {
       const int p = wave + kWideWaves * u;  // fragment p / 2, half p % 2
-      if (p < 2 * F)
-        copy_to_lds16(B + packed_fragment(F * tile + (p >> 1), kb, NT) + (p & 1) * 1024 + lane * 16, st + p * 1024);
+      if (p < 2 * F) dma_lds16(wsrc[u] + koff, ls + p * 1024);
     }
 #pragma unroll
-    for (int u = 0; u < TJ; ++u) copy_to_lds16(xa[u] + kb * 128, st + Sh::W + (wave + 8 * u) * 1024);
-    if (wave == 2) copy_to_lds4(ws_src + kb, st + Sh::WS);
+    for (int u = 0; u < TJ; ++u) dma_lds16(xa[u] + kb * 128, ls + Sh::W + (wave + 8 * u) * 1024);
+    if (wave == 2) dma_lds4(ws_src + kb, ls + Sh::WS);
     if (wave < TT && ((kb & 15) == 0 || kb == kb0)) {  // the window of kb: a buffer last used 16 blocks ago
       const int b = (kb & ~15) + sblk < KB ? (kb & ~15) + sblk : KB - 1;
-      uint8_t* win = smem + Sh::WIN + ((kb >> 4) & 1) * 8192 + wave * 1024;
+      const uint32_t win = lds0 + Sh::WIN + ((kb >> 4) & 1) * 8192 + wave * 1024;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) copy_to_lds4(Xs + static_cast<size_t>(srow[u]) * KB + b, win + u * 256);
+      for (int u = 0; u < 4; ++u) dma_lds4(Xs + static_cast<size_t>(srow[u]) * KB + b, win + u * 256);
     }
   };
   // MFMA operand of a token fragment in the swizzled layout: lane (r, g) reads chunks g
@@ -805,7 +832,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     // i - 2), and multiply block i.  Each wave always has the same number of its copies in
     // flight, so the wait counts are fixed.
     constexpr int SN = Sh::STAGES;
-    static_for<SN - 1>([&](auto j) { issue(last(decltype(j)::value), stage(decltype(j)::value)); });
+    static_for<SN - 1>([&](auto j) { issue(last(decltype(j)::value), decltype(j)::value); });
     wait_vm_ops((SN - 2) * ops);  // block 0 landed
     asm volatile("s_barrier" ::: "memory");
     Ops o0, o1;
@@ -813,7 +840,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     auto step = [&](int i, const Ops& cur, Ops& nxt) {
       wait_vm_ops((SN - 3) * ops);  // block i + 1 landed (blocks i + 2 .. i + SN - 2 may not have)
       asm volatile("s_barrier" ::: "memory");
-      issue(last(i + SN - 1), stage(i + SN - 1));
+      issue(last(i + SN - 1), (i + SN - 1) % SN);
       load(i + 1, nxt);  // unconditional (past the range it reads a stage unused): no
       mma(cur);          // branch, so the wait for cur's reads stays partial
     };
