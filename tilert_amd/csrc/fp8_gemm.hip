@@ -608,10 +608,11 @@ __global__ __launch_bounds__(kTiledWaves * 64) void fp8_gemm_tiled_kernel(
 // Per K block the weight fragments, the activation rows (read from x [M, K] itself) and
 // their scales are copied global -> LDS (global_load_lds, no registers) into a 4-stage
 // ring; each wave reads block i + 1's operands into a second register set while
-// block i's MFMAs run.  The 2F weight pieces are dealt to the waves round robin and three
-// waves copy the scales, so per-wave copy counts differ, but each wave issues the same
-// count every block and waits for its own copies with a fixed s_waitcnt before the
-// block's s_barrier.
+// block i's MFMAs run.  The 2F weight pieces are dealt to the waves round robin, wave 2
+// copies the weight scales and the token scales come in 16-block windows, so per-wave copy
+// counts differ, but each wave issues the same count every block (plus the window copies
+// at a window's first block, which only make the next waits stricter) and waits for its
+// own copies with a fixed s_waitcnt before the block's s_barrier.
 // Workgroup ids: the token groups of one weight slice (row tile, K range) are 8 ids apart,
 // so that, with consecutive ids dealt to the 8 XCDs round robin, both run on one XCD and
 // the second read of each weight fragment hits its L2 (FETCH_SIZE at M = 256 up: 148 MB
@@ -634,7 +635,7 @@ constexpr int kWideGrid = 256;
 constexpr int kCpolSc1 = 16;            // buffer access cache policy: sc1
 constexpr int kRsrcWord3 = 0x00020000;  // buffer resource word 3: 32-bit data format
 
-// 8 waves: waves w and w + 4 (same SIMD) share token pair w % 4 and split the F rows
+// 8 waves: waves w and w + 4 (same SIMD) share token fragments w % 4 and split the F rows
 // (FH and F - FH), so each SIMD has two waves to hide the other's LDS and MFMA latencies.
 constexpr int kWideWaves = 8;
 
