@@ -715,7 +715,7 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   const int n = KB - kb0 < per ? KB - kb0 : per;  // >= 1 (host plan)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tp = wave & 3, rh = wave >> 2;  // token pair, row split
+  const int tp = wave & 3, rh = wave >> 2;  // token fragments group, row split
   const int r = lane & 15, g = lane >> 4;
   const int t0 = 16 * TT * tg;        // first token of the group
   const int tf0 = TT * tg + TJ * tp;  // this wave's first token fragment
