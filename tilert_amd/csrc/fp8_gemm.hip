@@ -665,21 +665,6 @@ __host__ __device__ constexpr int wide_ops(int F, int TJ, int w) {
   return (2 * F - w + kWideWaves - 1) / kWideWaves + TJ + (w == 2 ? 1 : 0);
 }
 
-// s_waitcnt needs an immediate: the wave-uniform count picks one of the possible waits
-// (every count a ring of these kernels can need, 1..24; larger ones wait for everything)
-__device__ inline void wait_vm_ops(int ops) {
-  switch (ops) {
-#define TL_WAIT_CASE(n) \
-  case n: __builtin_amdgcn_s_waitcnt(vmcnt_imm(n)); break;
-    TL_WAIT_CASE(1) TL_WAIT_CASE(2) TL_WAIT_CASE(3) TL_WAIT_CASE(4) TL_WAIT_CASE(5) TL_WAIT_CASE(6)
-    TL_WAIT_CASE(7) TL_WAIT_CASE(8) TL_WAIT_CASE(9) TL_WAIT_CASE(10) TL_WAIT_CASE(11) TL_WAIT_CASE(12)
-    TL_WAIT_CASE(13) TL_WAIT_CASE(14) TL_WAIT_CASE(15) TL_WAIT_CASE(16) TL_WAIT_CASE(17) TL_WAIT_CASE(18)
-    TL_WAIT_CASE(19) TL_WAIT_CASE(20) TL_WAIT_CASE(21) TL_WAIT_CASE(22) TL_WAIT_CASE(23) TL_WAIT_CASE(24)
-#undef TL_WAIT_CASE
-    default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0)); break;
-  }
-}
-
 // Load-to-LDS copies as in copy_to_lds16 / copy_to_lds4 (common.h), but taking the LDS
 // address as a wave-uniform 32-bit value already computed, with no generic-to-LDS pointer
 // conversion per copy (m0, a reserved register, is saved and restored as there): the wide
@@ -687,12 +672,12 @@ __device__ inline void wait_vm_ops(int ops) {
 __device__ inline void dma_lds16(const void* src, uint32_t lds) {
   uint32_t saved;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+               : "=&s"(saved) : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 __device__ inline void dma_lds4(const void* src, uint32_t lds) {
   uint32_t saved;
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(saved) : "v"(src), "s"(lds) : "memory");
+               : "=&s"(saved) : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
 }
 
 template <int F, int TJ>
@@ -791,8 +776,11 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
   // Operands of one K block for rows f0 .. f0 + NR - 1, read from LDS into registers.
   // The loop is software-pipelined over two such sets: block i + 1's fragments are read
   // while block i's MFMAs run, so LDS reads and matrix work overlap.
-  auto run = [&](auto nr_tag) {
+  // OPS: this wave's copies per block, a compile-time constant in each specialisation so
+  // that every wait is a single immediate s_waitcnt
+  auto run = [&](auto nr_tag, auto ops_tag) {
     constexpr int NR = decltype(nr_tag)::value;
+    constexpr int OPS = decltype(ops_tag)::value;
     struct Ops {
       v8i a[TJ], w[NR];
       float ts[TJ], ws[NR];
@@ -834,12 +822,12 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
     // flight, so the wait counts are fixed.
     constexpr int SN = Sh::STAGES;
     static_for<SN - 1>([&](auto j) { issue(last(decltype(j)::value), decltype(j)::value); });
-    wait_vm_ops((SN - 2) * ops);  // block 0 landed
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((SN - 2) * OPS));  // block 0 landed
     asm volatile("s_barrier" ::: "memory");
     Ops o0, o1;
     load(0, o0);
     auto step = [&](int i, const Ops& cur, Ops& nxt) {
-      wait_vm_ops((SN - 3) * ops);  // block i + 1 landed (blocks i + 2 .. i + SN - 2 may not have)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((SN - 3) * OPS));  // block i + 1 landed (not i + 2 .. i + SN - 2)
       asm volatile("s_barrier" ::: "memory");
       issue(last(i + SN - 1), (i + SN - 1) % SN);
       load(i + 1, nxt);  // unconditional (past the range it reads a stage unused): no
@@ -850,8 +838,17 @@ __global__ __launch_bounds__(kWideWaves * 64) void fp8_gemm_wide_kernel(
       if (i + 1 < n) step(i + 1, o1, o0);
     }
   };
-  if (rh == 0) run(std::integral_constant<int, FH>{});
-  else run(std::integral_constant<int, F - FH>{});
+  // the wave's copy count takes one of at most three consecutive values (weight pieces
+  // differ by one between waves, wave 2 adds the weight scales)
+  constexpr int OPS_LO = wide_ops(F, TJ, kWideWaves - 1);
+  static_assert(wide_ops(F, TJ, 0) <= OPS_LO + 1 && wide_ops(F, TJ, 2) <= OPS_LO + 2, "copy counts");
+  auto by_ops = [&](auto nr_tag) {
+    if (ops == OPS_LO) run(nr_tag, std::integral_constant<int, OPS_LO>{});
+    else if (ops == OPS_LO + 1) run(nr_tag, std::integral_constant<int, OPS_LO + 1>{});
+    else run(nr_tag, std::integral_constant<int, OPS_LO + 2>{});
+  };
+  if (rh == 0) by_ops(std::integral_constant<int, FH>{});
+  else by_ops(std::integral_constant<int, F - FH>{});
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // no copy may land after the workgroup ends
 
   // lane holds rows 16 (F tile + f0 + f) + 4 g + (0..3) of token 16 (tf0 + j) + r
