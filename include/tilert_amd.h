@@ -200,8 +200,9 @@ int tl_moe_down_combine(const void* h_bf16, const void* w2_packed, const float* 
  * stacked [n_local * 2I, D] gate/up (per expert I gate rows, then I up rows) and
  * [n_local * D, I] down matrices; fp32 block scales [n_local, 2I/128, D/128] and
  * [n_local, D/128, I/128].  bf16 activations times bf16(fp32(q) * scale) weights, fp32
- * accumulation (the goldens' bf16 reference weights).  At most 64 (token, position) pairs,
- * x [M, D] within 64 KB (M <= 4 at D = 7168). */
+ * accumulation (the goldens' bf16 reference weights).  1 <= M <= 16 tokens (one 16-row MFMA
+ * tile), at most 64 (token, position) pairs, x [M, D] within 64 KB (M <= 4 at D = 7168).
+ * With a bias and n_groups > 1 every group holds >= 2 experts. */
 
 /* Routing of expert_select_up_gate_silu_op (golden _ref_expert_select_ds,
  * glm_5/_dsa_v32/ops/expert_sel_up_gate_silu.py:714-737; n_groups = 1 is

@@ -70,6 +70,35 @@ def test_argument_errors_need_no_gpu():
     assert lib.tl_projx_wqkva(None, None, None, None, None, None, None, None, 2, 40, 128, 7168, 1536, 512, 64, None, 0, None) == 3
 
 
+def test_reference_layout_moe_rejects_more_than_one_row_tile():
+    """The reference-layout gate/up and down kernels compute one 16-token MFMA tile: M > 16
+    must fail before any launch (M = 32 at 2 chunks is within the 64-pair limit)."""
+    from tilert_amd import _lib
+    lib = _lib.load()
+    assert lib.tl_down_allreduce(None, None, None, None, 32, 2, 7168, 256, None, None) == 3
+    assert b"> 16 tokens" in lib.tl_last_error()
+    assert lib.tl_rmsnorm_up_gate_silu(None, None, 1e-6, None, None, 17, 1, 7168, 256, None, None) == 3
+    assert lib.tl_expert_down_allreduce(None, None, None, None, None, None, 32, 256, 1, 7168, 256, None, None) == 3
+    assert lib.tl_expert_select_up_gate_silu(None, None, None, None, None, 21, 256, 2, 8, 4, 2.5, 7168, 256,
+                                             None, None, None, None) == 3
+    # M = 16 passes the shape checks and stops at the null pointers
+    assert lib.tl_down_allreduce(None, None, None, None, 16, 2, 7168, 256, None, None) == 1
+    assert b"null pointer" in lib.tl_last_error()
+
+
+def test_routing_with_bias_needs_two_experts_per_group():
+    """With a bias a group scores as its two best experts' sum: one-expert groups are rejected
+    (the reference's topk(2) over a group would raise); without a bias they are fine."""
+    import ctypes
+    from tilert_amd import _lib
+    lib = _lib.load()
+    bias = ctypes.c_void_p(16)  # any non-null value: validation happens before any device access
+    assert lib.tl_moe_route(None, bias, 4, 8, 2, 8, 4, 1.0, None, None, None) == 1
+    assert b">= 2 experts" in lib.tl_last_error()
+    assert lib.tl_moe_route(None, None, 4, 8, 2, 8, 4, 1.0, None, None, None) == 1
+    assert b"null pointer" in lib.tl_last_error()
+
+
 def test_wrappers_reject_cpu_tensors():
     from tilert_amd import kernel as K
     from tilert_amd.topk import topk_accurate

@@ -440,6 +440,8 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
 
 static int check_common(const char* who, int64_t M, int64_t P, int64_t D, int64_t I) {
   if (M < 1 || M * P > 64) { set_error("%s: M=%lld with %lld positions per token: at most 64 pairs", who, (long long)M, (long long)P); return kErrUnsupported; }
+  // The gate/up and down kernels compute one 16-token MFMA row tile (token r = lane & 15).
+  if (M > 16) { set_error("%s: M=%lld > 16 tokens (one 16-row MFMA tile per call)", who, (long long)M); return kErrUnsupported; }
   if (D <= 0 || I <= 0 || D % kBlock || I % kBlock) { set_error("%s: D=%lld and I=%lld must be positive multiples of 128", who, (long long)D, (long long)I); return kErrArg; }
   if (D > (1 << 16) || I > (1 << 16)) { set_error("%s: D or I too large", who); return kErrArg; }
   return kOk;
@@ -484,12 +486,15 @@ static int launch_down(bool dense, const void* h, const void* w2, const float* s
   return check_launch("down");
 }
 
-static int check_routing(const char* who, int64_t M, int64_t n_routed, int64_t topk, int64_t n_groups, int64_t topk_groups) {
+static int check_routing(const char* who, int64_t M, int64_t n_routed, int64_t topk, int64_t n_groups, int64_t topk_groups,
+                         bool has_bias) {
   if (M < 1 || M > 65535) { set_error("%s: M=%lld out of range", who, (long long)M); return kErrArg; }
   if (n_routed < 1 || n_routed > kRefMaxRouted) { set_error("%s: n_routed=%lld must be in [1, %d]", who, (long long)n_routed, kRefMaxRouted); return kErrUnsupported; }
   if (n_groups < 1 || n_groups > 64 || n_routed % n_groups) { set_error("%s: n_groups=%lld must divide n_routed=%lld (<= 64 groups)", who, (long long)n_groups, (long long)n_routed); return kErrArg; }
   if (topk_groups < 1 || topk_groups > n_groups) { set_error("%s: topk_groups=%lld must be in [1, n_groups]", who, (long long)topk_groups); return kErrArg; }
   if (topk < 1 || topk > 64 || topk > topk_groups * (n_routed / n_groups)) { set_error("%s: topk=%lld exceeds the experts of the kept groups", who, (long long)topk); return kErrArg; }
+  // With a bias a group scores as the sum of its two best experts: groups need two experts.
+  if (has_bias && n_groups > 1 && n_routed / n_groups < 2) { set_error("%s: with a bias each of the n_groups=%lld groups needs >= 2 experts", who, (long long)n_groups); return kErrArg; }
   return kOk;
 }
 
@@ -500,7 +505,7 @@ using namespace tl;
 extern "C" int tl_moe_route(const float* scores, const float* bias, int64_t M, int64_t n_routed, int64_t topk,
                             int64_t n_groups, int64_t topk_groups, float route_scale, float* probs_out, int32_t* idx_out,
                             void* stream) {
-  if (int rc = check_routing("moe_route", M, n_routed, topk, n_groups, topk_groups)) return rc;
+  if (int rc = check_routing("moe_route", M, n_routed, topk, n_groups, topk_groups, bias != nullptr)) return rc;
   if (!scores || !probs_out || !idx_out) { set_error("moe_route: null pointer"); return kErrArg; }
   hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(M)), dim3(64), 0, (hipStream_t)stream, scores, bias,
                      (int)n_routed, (int)topk, (int)n_groups, (int)topk_groups, route_scale, probs_out, idx_out);
@@ -513,7 +518,7 @@ extern "C" int tl_expert_select_up_gate_silu(const void* x_bf16, const float* sc
                                              int64_t D, int64_t I, void* h_bf16, float* probs_out, int32_t* idx_out,
                                              void* stream) {
   const char* who = "expert_select_up_gate_silu";
-  if (int rc = check_routing(who, M, n_routed, topk, n_groups, topk_groups)) return rc;
+  if (int rc = check_routing(who, M, n_routed, topk, n_groups, topk_groups, bias != nullptr)) return rc;
   if (int rc = check_common(who, M, 1 + topk, D, I)) return rc;
   if (!x_bf16 || !scores || !w13_packed || !s13 || !h_bf16 || !probs_out || !idx_out) { set_error("%s: null pointer", who); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed) | reinterpret_cast<uintptr_t>(h_bf16)) & 15) {
@@ -551,7 +556,6 @@ extern "C" int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, f
   const char* who = "rmsnorm_up_gate_silu";
   if (n_chunks < 1 || n_chunks > kRefMaxLocal) { set_error("%s: n_chunks=%lld out of range", who, (long long)n_chunks); return kErrArg; }
   if (int rc = check_common(who, M, n_chunks, D, I)) return rc;
-  if (M > 16) { set_error("%s: M=%lld > 16", who, (long long)M); return kErrUnsupported; }
   if (!x_bf16 || !gamma || !w13_packed || !s13 || !h_bf16) { set_error("%s: null pointer", who); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w13_packed) | reinterpret_cast<uintptr_t>(gamma) |
        reinterpret_cast<uintptr_t>(h_bf16)) & 15) {
