@@ -3,9 +3,11 @@
 * ``projx_wqaki``: x_q . [wq_a; wk]^T routed to q and ki -- each output equals the FP8 GEMM
   oracle on its own weight at the GEMM bar;
 * ``projx_wis``: the bf16 weights_proj GEMV at the GEMM bar;
-* ``rmsnorm_projx_wqakis`` (decoupled): the three outputs against the module's fp32 golden
-  (rms_norm, then fp32 matmuls) at rel-L2 3e-2 -- the kernels quantise the normalised rows to
-  fp8 for wq_a / wk, which the golden does not;
+* ``rmsnorm_projx_wqakis`` (decoupled): q and ki at the GEMM bar against the oracle chain
+  that the module runs (``rmsnorm_quant``: bf16 norm, act_quant; then the FP8 GEMM),
+  idx_scores at the GEMM bar against ``projx_wis`` of the oracle's bf16 norm; and the three
+  outputs against the module's fp32 golden (rms_norm, then fp32 matmuls) at rel-L2 3e-2 --
+  the kernels quantise the normalised rows to fp8 for wq_a / wk, which the golden does not;
 * ``rmsnorm_projq_wqi_op``: the golden (bf16 normalised q, bf16 weights) at the GEMM bar,
   64 heads x 128 at q_lora 1536 (DeepSeek-V3.2) and 2048 (GLM-5), s in 1, 2, 4, 8."""
 import pytest
@@ -54,9 +56,9 @@ def test_projx_wqaki_and_wis_vs_oracle(cuda, dim, q_rank, M):
     assert_gemm_close(sc[0], ref.projx_wis(x, wis), "idx_scores")
 
 
-@pytest.mark.parametrize("arch,dim,q_rank", [("deepseek_v3_2", 7168, 1536), ("glm_5", 6144, 2048)])
-def test_rmsnorm_projx_wqakis_vs_golden(cuda, arch, dim, q_rank):
-    M = 4
+@pytest.mark.parametrize("arch,dim,q_rank,M", [("deepseek_v3_2", 7168, 1536, 4), ("glm_5", 6144, 2048, 4),
+                                                 ("deepseek_v3_2", 7168, 1536, 1), ("deepseek_v3_2", 7168, 1536, 16)])
+def test_rmsnorm_projx_wqakis_vs_golden(cuda, arch, dim, q_rank, M):
     wq, wqs, wk, wks, wis = _weights(dim, q_rank, 5 + dim)
     g = synth.gen(77)
     x = synth.activations(M, dim, g)
@@ -68,6 +70,12 @@ def test_rmsnorm_projx_wqakis_vs_golden(cuda, arch, dim, q_rank):
     rmsnorm_projx_wqakis(x.reshape(1, M, dim).to(cuda), gamma.to(cuda), packed, wis.to(cuda), q, ki, sc,
                          model_arch=arch)
     eps = 1e-6 if arch == "deepseek_v3_2" else 1e-5
+    # the chain the module runs, restated: bf16 norm + act_quant, then the FP8 GEMM / bf16 GEMV
+    y, xq, xs = ref.rmsnorm_quant(x, gamma, eps)
+    assert_gemm_close(q[0], ref.fp8_gemm(xq, xs, wq, wqs), f"q {arch}")
+    assert_gemm_close(ki[0], ref.fp8_gemm(xq, xs, wk, wks), f"ki {arch}")
+    assert_gemm_close(sc[0], ref.projx_wis(y, wis), f"idx_scores {arch}")
+    # the module's fp32 golden
     rq, rki, rsc = ref.rmsnorm_projx_wqakis(x, gamma, wq, wqs, wk, wks, wis, eps)
     assert _rel(q[0], rq) <= 3e-2 and _rel(ki[0], rki) <= 3e-2
     assert _rel(sc[0], rsc) <= 1e-2  # bf16 rows, bf16 weights: no fp8 step

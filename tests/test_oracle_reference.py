@@ -506,3 +506,66 @@ def test_absorbed_mla_goldens_vs_fp64_loops():
     y = ref.unproj_o_allreduce(x, wo, wos, bf16_weights=False, x_in=xin)
     want = x.reshape(T, -1).double() @ ref.weight_dequant(wo, wos).double().T + xin[0].double()
     assert torch.allclose(y[0].double(), want, rtol=2e-2, atol=2e-2)
+
+
+# ------------------------------------------------------- the indexer's projections
+def test_projx_wis_vs_fp64_and_one_hot_rows():
+    """projx_wis is x . W^T with bf16 operands: fp64 loops over (token, head), one-hot weight
+    rows that must pick one input column each (a transposed weight or swapped output axis
+    picks the wrong one), and a non-square shape so a transpose cannot type-check."""
+    g = synth.gen(48)
+    T, H, D = 3, 5, 384
+    x = synth.activations(T, D, g)
+    w = (torch.randn(H, D, generator=g) * 0.05).to(torch.bfloat16)
+    got = ref.projx_wis(x, w)
+    assert got.shape == (T, H) and got.dtype == torch.bfloat16
+    xd, wd = x.double(), w.double()
+    for t in range(T):
+        for h in range(H):
+            want = sum(float(xd[t, k]) * float(wd[h, k]) for k in range(D))
+            assert abs(float(got[t, h]) - want) <= 2.0 ** -8 * abs(want) + 1e-6
+    cols = [7, 0, 383, 200, 129]
+    one = torch.zeros(H, D, dtype=torch.bfloat16)
+    for h, c in enumerate(cols):
+        one[h, c] = 1.0
+    assert torch.equal(ref.projx_wis(x, one), x[:, cols])
+
+
+def test_rmsnorm_projx_wqakis_vs_fp64_brute_force():
+    """The golden's three outputs against fp64 brute force: fp64 RMSNorm (gamma applied per
+    column), then the fp64 block-scaled dot products with wq_a and wk (decoded e4m3 codes
+    times their block scales) and the bf16 weights_proj.  A one-hot gamma row and a one-hot
+    weights_proj row pin which column each output reads."""
+    g = synth.gen(49)
+    T, D, QR = 2, 256, 256
+    x = synth.activations(T, D, g)
+    gamma = torch.rand(D, generator=g) + 0.5
+    wq, wqs = ref.weight_quant(synth.weight_fp32(QR, D, g))
+    wk, wks = ref.weight_quant(synth.weight_fp32(128, D, g) * 3)
+    wis = (torch.randn(4, D, generator=g) * 0.05).to(torch.bfloat16)
+    eps = 1e-6
+    q, ki, sc = ref.rmsnorm_projx_wqakis(x, gamma, wq, wqs, wk, wks, wis, eps)
+    assert q.shape == (T, QR) and ki.shape == (T, 128) and sc.shape == (T, 4)
+    xd = x.double().numpy()
+    xn = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + eps) * gamma.double().numpy()
+
+    def dense(codes, s):
+        w = fp8.decode(codes.view(torch.uint8).numpy()).astype(np.float64)
+        sn = s.double().numpy()
+        for r in range(w.shape[0]):
+            for kb in range(w.shape[1] // 128):
+                w[r, kb * 128:(kb + 1) * 128] *= sn[r // 128, kb]
+        return w
+
+    for got, want in ((q, xn @ dense(wq, wqs).T), (ki, xn @ dense(wk, wks).T),
+                      (sc, xn @ wis.double().numpy().T)):
+        got = got.double().numpy()
+        ulp = 2.0 ** (np.floor(np.log2(np.abs(want) + 1e-30)) - 7)
+        assert np.all(np.abs(got - want) <= 0.5 * ulp + 1e-5 * np.abs(want) + 1e-30)
+    # weights_proj row h = e_c reads the normalised column c
+    one = torch.zeros(4, D, dtype=torch.bfloat16)
+    for h, c in enumerate((3, 100, 255, 128)):
+        one[h, c] = 1.0
+    _, _, sc1 = ref.rmsnorm_projx_wqakis(x, gamma, wq, wqs, wk, wks, one, eps)
+    want1 = torch.from_numpy(xn[:, [3, 100, 255, 128]]).to(torch.bfloat16)
+    assert (sc1.double() - want1.double()).abs().max() <= 2.0 ** -7 * want1.double().abs().max()
