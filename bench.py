@@ -32,11 +32,12 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
 WARMUP_MIN_S = 0.2
 CALLS = 20          # calls per captured graph for every configuration but the headline
 MOE_ROUTINGS = CALLS  # config 2's routings: fixed, whatever --steps is
 SECTIONS = ("headline", "moe_ep8_M4", "indexer_topk_128k_M4", "mla_projections_M4", "m_sweep", "ref_layout",
-            "extras")
+            "indexer_bf16", "extras")
 METRIC = "µs/call + achieved HBM GB/s (% of peak) for FP8 block-scaled GEMM at M=4"
 
 
@@ -287,15 +288,15 @@ def bench_indexer(torch, dev, cpu=True, keep=False):
     q, qsc, w = indexer_queries(torch, dev, gk, M, H)
     logits = torch.empty(M, L, device=dev)
     idx = torch.empty(M, k, dtype=torch.int32, device=dev)
-    us_s = _graph_time_us(torch, lambda i: si.sparse_index(q, qsc, caches[i % 20][0], caches[i % 20][1], w, logits,
+    us_s = _graph_time_us(torch, lambda i: si.sparse_index_fp8(q, qsc, caches[i % 20][0], caches[i % 20][1], w, logits,
                                                            L - 4), st, 5)
     us_k = _graph_time_us(torch, lambda i: topk_rows(logits, L - 4, k, out=idx), st, 5)
-    us_b = _graph_time_us(torch, lambda i: si.sparse_index_topk(q, qsc, caches[i % 20][0], caches[i % 20][1], w,
+    us_b = _graph_time_us(torch, lambda i: si.sparse_index_topk_fp8(q, qsc, caches[i % 20][0], caches[i % 20][1], w,
                                                                 logits, idx, L - 4), st, 5)
     b_s = L * 128 + L * 4 + M * H * 128 + M * 4 + M * H * 2 + M * L * 4
-    b_all = b_s + M * L * 4 + M * k * 4  # + logits read back by top-k, indices written
+    b_all = b_s + M * L * 4 + M * k * 4  # + logits read back by the selection, indices written
     flops = 2 * M * H * 128 * L
-    res = {"us": round(us_b, 2), "scores_us": round(us_s, 2), "topk_us": round(us_k, 2),
+    res = {"us": round(us_b, 2), "launches": 2, "scores_us": round(us_s, 2), "topk_us": round(us_k, 2),
            "bytes_per_call": b_all, "GBs": round(b_all / us_b / 1e3, 1),
            "hbm_frac": round(b_all / us_b / 1e3 / HBM_PEAK_GBS, 4),
            "scores_hbm_frac": round(b_s / us_s / 1e3 / HBM_PEAK_GBS, 4),
@@ -305,7 +306,7 @@ def bench_indexer(torch, dev, cpu=True, keep=False):
                         "traffic": measured_traffic("indexer_topk_128k_M4.md"),
                         "traffic_source": "profiles/indexer_topk_128k_M4.md (rocprofv3 --pmc FETCH_SIZE, "
                                           "WRITE_SIZE; indexer + top-k per call)",
-                        "kernel": "tl::indexer_kernel + tl::topk_kernel", "bytes_per_call": b_all}}
+                        "kernel": "tl::indexer_kernel<4, 64, 16, 0> + tl::topk_kernel<4>", "bytes_per_call": b_all}}
     if cpu:
         # the reference torch path on the host cores: fp32 einsum of the dequantised q and
         # keys, ReLU, head-weighted sum, causal mask, torch.topk (ops/topk.py:128-143)
@@ -330,6 +331,32 @@ def bench_indexer(torch, dev, cpu=True, keep=False):
     del caches
     torch.cuda.empty_cache()
     return res
+
+
+def bench_indexer_bf16(torch, dev):
+    """The reference's own bf16 indexer operators at 128K keys, M = 4, top-2048:
+    sparse_index_topk (DeepSeek-V3.2, 64 heads) and sparse_index_topk_v3 (GLM-5, 32 heads),
+    each one call (scores, then the exact top-k); 10 rotating bf16 caches (335 MB)."""
+    from tilert_amd import sparse_index as si
+    from tilert_amd.sparse_index_v3 import sparse_index_topk_v3
+    M, L, k = 4, 131072, 2048
+    g = torch.Generator().manual_seed(31)
+    caches = [randn(torch, (1, L, 128), g, dev).to(torch.bfloat16) for _ in range(10)]
+    logits = torch.empty(1, M, L, device=dev)
+    idx = torch.empty(1, M, k, dtype=torch.int32, device=dev)
+    out = {}
+    for name, H, op in (("indexer_bf16_topk_dsv32_128k_M4", 64, si.sparse_index_topk),
+                        ("indexer_bf16_topk_v3_glm5_128k_M4", 32, sparse_index_topk_v3)):
+        q = randn(torch, (1, M, H, 128), g, dev).to(torch.bfloat16)
+        w = randn(torch, (1, M, H), g, dev, 1 / 8).to(torch.bfloat16)
+        us = _graph_time_us(torch, lambda i: op(q, caches[i % 10], w, logits, idx, L - 4, None), CALLS, 5)
+        b = L * 256 + M * H * 256 + M * H * 2 + 2 * M * L * 4 + M * k * 4
+        flops = 2 * M * H * 128 * L
+        out[name] = {"us": round(us, 2), "launches": 2, "bytes_per_call": b, "GBs": round(b / us / 1e3, 1),
+                     "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                     "mfma_util_bf16": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del caches
+    return out
 
 
 def _stack_quant(torch, n, k, cnt, g, dev):
@@ -739,6 +766,9 @@ def main() -> int:
         configs.update(bench_ref_layout(torch, dev))
         torch.cuda.empty_cache()
         progress("ref_layout")
+    if want("indexer_bf16"):
+        configs.update(bench_indexer_bf16(torch, dev))
+        progress("indexer_bf16")
     if configs:
         res["configs"] = configs
     if want("extras"):

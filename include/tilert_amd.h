@@ -48,7 +48,10 @@
  *   tl_flash_sparse_mla    flash_sparse_mla_op            .../ops/flash_sparse_mla.py:18-93
  *                          (golden FlashSparseMLACombine.golden_forward :152-196)
  *   tl_topk_rows           topk_accurate_op               .../ops/topk.py:62-109
- *   (sparse_index_topk_dsv32_op, .../ops/sparse_index.py:72-128, = scores + top-k)
+ *   tl_indexer_fp8_topk    sparse_index_topk_dsv32_op (fp8 cache)  .../ops/sparse_index.py:72-128
+ *   tl_indexer_bf16_scores sparse_index_op (bf16, the reference's own)  .../ops/sparse_index.py:11-69
+ *   tl_indexer_bf16_topk   sparse_index_topk_dsv32_op  .../ops/sparse_index.py:72-128 and
+ *                          sparse_index_topk_glm5_v3_op  glm_5/ops/sparse_index_v3.py:10-51
  */
 #ifndef TILERT_AMD_H_
 #define TILERT_AMD_H_
@@ -314,6 +317,37 @@ int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per
                                 const void* ki_pages, int64_t n_pages, const void* w_bf16,
                                 float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
                                 int64_t cur_pos, void* stream);
+
+/* sparse_index_topk as one call (sparse_index_topk_dsv32_op, ops/sparse_index.py:72-128; the
+ * selection is topk_accurate's, ops/topk.py:62-109): the scores of tl_indexer_fp8_scores into
+ * logits, then on the same stream indices int32 [M, topk] = the exact top-topk key positions
+ * of each token's visible keys 0 .. cur_pos + t, ascending, ties at the threshold to the
+ * lowest positions, -1 past the visible count (tl_topk_rows with valid_base = cur_pos).
+ * topk <= 8192, ld % 4 == 0, ld <= 262144, logits 16-byte aligned.  workspace: at least
+ * tl_indexer_topk_workspace_bytes(M, ld, topk) bytes (= tl_topk_workspace_bytes), zero-filled
+ * once before its first use; every call leaves it reusable, so calls of any shapes in stream
+ * order may share one (calls that overlap on one workspace race). */
+size_t tl_indexer_topk_workspace_bytes(int64_t M, int64_t ld, int64_t topk);
+int tl_indexer_fp8_topk(const void* q_fp8, const float* q_s, int q_s_per_head, const void* k_fp8,
+                        const float* k_s, const void* w_bf16, float* logits, int64_t M, int64_t H,
+                        int64_t L, int64_t ld, int64_t cur_pos, int64_t topk, int32_t* indices,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* The reference's bf16 indexer (sparse_index_op, ops/sparse_index.py:11-69): q bf16
+ * [M, H, 128], k bf16 [L, 128] (the index-key cache), w bf16 [M, H]; logits[t, l] =
+ * score_scale * sum_h w[t,h] * ReLU(q[t,h] . k[l]) in fp32 (bf16 MFMA) for l <= cur_pos + t,
+ * -inf for cur_pos + t < l < L.  H in {32, 64}, M*H <= 256; q, k 16-byte aligned. */
+int tl_indexer_bf16_scores(const void* q_bf16, const void* k_bf16, const void* w_bf16, float score_scale,
+                           float* logits, int64_t M, int64_t H, int64_t L, int64_t ld, int64_t cur_pos,
+                           void* stream);
+
+/* tl_indexer_bf16_scores and the top-k of tl_indexer_fp8_topk as one call:
+ * sparse_index_topk_dsv32_op (H = 64, ops/sparse_index.py:72-128) and
+ * sparse_index_topk_glm5_v3_op (H = 32, glm_5/ops/sparse_index_v3.py:10-51). */
+int tl_indexer_bf16_topk(const void* q_bf16, const void* k_bf16, const void* w_bf16, float score_scale,
+                         float* logits, int64_t M, int64_t H, int64_t L, int64_t ld, int64_t cur_pos,
+                         int64_t topk, int32_t* indices, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* Write `rows` keys (bf16 [rows, 128]) into KI pages at positions pos .. pos+rows-1:
  * per key s = the act_quant group scale of its amax (scale_mode as tl_act_quant), fp8 =

@@ -266,6 +266,22 @@ def indexer_scores(
     return torch.where(pos <= lim, score, torch.tensor(float("-inf")))
 
 
+def indexer_scores_bf16(q: torch.Tensor, k: torch.Tensor, w: torch.Tensor, cur_pos: int,
+                        score_scale: float) -> torch.Tensor:
+    """The reference's bf16 indexer (``sparse_index``, ops/sparse_index.py:11-69: "q * kv *
+    weights"; bf16 q [M,H,128], bf16 key cache [L,128], bf16 head weights [M,H]), fp32 [M, L]:
+    ``score_scale * sum_h w[t,h] * ReLU(q[t,h] . k[l])`` in fp32, -inf for l > cur_pos + t.
+    ``score_scale`` is the constant the operator applies inside the kernel ("we precompute
+    scale inner kernel", :58-59); this build uses (128 H)^-1/2."""
+    M, H, _ = q.shape
+    L = k.shape[0]
+    logits = torch.relu(torch.einsum("thd,ld->thl", q.float(), k.float()))
+    score = torch.einsum("thl,th->tl", logits, w.float()) * score_scale
+    pos = torch.arange(L)[None, :]
+    lim = (cur_pos + torch.arange(M))[:, None]
+    return torch.where(pos <= lim, score, torch.tensor(float("-inf")))
+
+
 def topk_rows(logits: torch.Tensor, valid: list[int], k: int) -> torch.Tensor:
     """Per-row top-k indices among the first ``valid[i]`` columns, int32 [rows, k].
 

@@ -41,7 +41,7 @@ def test_moe_fixture_gpu(cuda):
 def test_indexer_fixture_gpu(cuda):
     d = load("indexer")
     logits = torch.empty(2, 512, device=cuda)
-    si.sparse_index(fp8(d["q_fp8"]).to(cuda), f32(d["q_s"]).to(cuda), fp8(d["k_fp8"]).to(cuda),
+    si.sparse_index_fp8(fp8(d["q_fp8"]).to(cuda), f32(d["q_s"]).to(cuda), fp8(d["k_fp8"]).to(cuda),
                     f32(d["k_s"]).to(cuda), bf16(d["w_bf16"]).to(cuda), logits, int(d["cur_pos"]))
     want = f32(d["logits"])
     got = logits.cpu()

@@ -79,7 +79,7 @@ def test_indexer_topk_graph_replays(cuda):
     idx = torch.empty(M, k, dtype=torch.int32, device=cuda)
 
     def run():
-        si.sparse_index_topk(q, qs, kv, ks, w, logits, idx, L - M)
+        si.sparse_index_topk_fp8(q, qs, kv, ks, w, logits, idx, L - M)
         return [logits, idx]
 
     _check_replays(run)

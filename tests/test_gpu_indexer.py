@@ -43,7 +43,7 @@ def test_indexer_scores_vs_oracle(cuda, M, H, L, cur_pos, per_head):
         qs = (torch.rand(M, H, generator=g) + 0.5) * qs[:, None]
     ld = L + 8
     logits = torch.full((M, ld), 7.0, device=cuda)
-    si.sparse_index(q.to(cuda), qs.to(cuda).contiguous(), k.to(cuda), ks.to(cuda), w.to(cuda), logits, cur_pos)
+    si.sparse_index_fp8(q.to(cuda), qs.to(cuda).contiguous(), k.to(cuda), ks.to(cuda), w.to(cuda), logits, cur_pos)
     want = ref.indexer_scores(q, qs, k, ks, w, cur_pos)
     _scores_close(logits[:, :L], want)
     assert torch.all(logits[:, L:].cpu() == 7.0), "columns past L must be untouched"
@@ -176,7 +176,7 @@ def test_sparse_index_topk_128k(cuda):
     q, qs, kk, ks, w = synth.indexer_inputs(M, H, L, g)
     logits = torch.empty(M, L, device=cuda)
     idx = torch.empty(M, k, dtype=torch.int32, device=cuda)
-    si.sparse_index_topk(q.to(cuda), qs.to(cuda), kk.to(cuda), ks.to(cuda), w.to(cuda), logits, idx, L - 4)
+    si.sparse_index_topk_fp8(q.to(cuda), qs.to(cuda), kk.to(cuda), ks.to(cuda), w.to(cuda), logits, idx, L - 4)
     want = ref.indexer_scores(q, qs, kk, ks, w, L - 4)
     _scores_close(logits, want)
     _assert_topk_set(idx, want, [L - 3, L - 2, L - 1, L], k)
@@ -199,7 +199,7 @@ def test_paged_indexer_matches_flat(cuda, M, H, L, cur_pos, per_head):
     pages = si.ki_pages_from_flat(k, ks)
     flat = torch.full((M, L + 8), 7.0, device=cuda)
     paged = torch.full((M, L + 8), 7.0, device=cuda)
-    si.sparse_index(q, qs, k, ks, w, flat, cur_pos)
+    si.sparse_index_fp8(q, qs, k, ks, w, flat, cur_pos)
     si.sparse_index_paged(q, qs, pages, w, paged, cur_pos, L)
     assert torch.equal(flat, paged)
     if L <= 5000:
@@ -243,6 +243,6 @@ def test_ki_write_then_paged_scores(cuda):
     kq, ks = K.act_quant(keys, scale_fmt="div")
     flat = torch.empty(M, L, device=cuda)
     paged = torch.empty(M, L, device=cuda)
-    si.sparse_index(q, qs, kq, ks.reshape(-1).contiguous(), w, flat, L - 4)
+    si.sparse_index_fp8(q, qs, kq, ks.reshape(-1).contiguous(), w, flat, L - 4)
     si.sparse_index_paged(q, qs, pages, w, paged, L - 4, L)
     assert torch.equal(flat, paged)

@@ -168,6 +168,33 @@ def test_indexer_scale_factoring_identity():
     assert torch.allclose(b, a * 4, rtol=1e-6, atol=0)
 
 
+def test_bf16_indexer_vs_fp64_brute_force_and_one_hot():
+    """The bf16 indexer against fp64 loops over (token, key, head), the causal -inf
+    pattern, the score scale as a plain factor, and a one-hot query/weight that must read
+    one key element back (a transposed contraction or a wrong head index fails it)."""
+    M, H, L, cur, sc = 3, 32, 50, 44, 0.0625
+    g = synth.gen(10)
+    q = torch.randn(M, H, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(L, 128, generator=g).to(torch.bfloat16)
+    w = (torch.randn(M, H, generator=g) / 8).to(torch.bfloat16)
+    got = ref.indexer_scores_bf16(q, k, w, cur, sc).double()
+    qd, kd, wd = q.double(), k.double(), w.double()
+    for t in range(M):
+        for l in range(L):
+            if l > cur + t:
+                assert got[t, l] == float("-inf")
+                continue
+            want = sc * sum(float(wd[t, h]) * max(0.0, float(qd[t, h] @ kd[l])) for h in range(H))
+            assert abs(float(got[t, l]) - want) <= 1e-5 * (1 + abs(want))
+    # one-hot: token 0 has head 3 = e_17 with weight 1, all other heads zero
+    q1 = torch.zeros(1, H, 128, dtype=torch.bfloat16)
+    q1[0, 3, 17] = 1.0
+    w1 = torch.zeros(1, H, dtype=torch.bfloat16)
+    w1[0, 3] = 1.0
+    one = ref.indexer_scores_bf16(q1, k, w1, L - 1, 1.0)[0]
+    assert torch.equal(one, torch.relu(k[:, 17].float()))
+
+
 # --------------------------------------------------------------------------- top-k
 def test_topk_vs_selection_brute_force_with_ties():
     g = synth.gen(9)

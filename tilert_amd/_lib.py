@@ -66,6 +66,13 @@ SIGNATURES: dict[str, tuple] = {
     "tl_indexer_fp8_scores_paged": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _i64,
                                            _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                            _c_void_p]),
+    "tl_indexer_topk_workspace_bytes": (_size, [_i64, _i64, _i64]),
+    "tl_indexer_fp8_topk": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                   _i64, _i64, _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _size, _c_void_p]),
+    "tl_indexer_bf16_scores": (_int, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _i64, _i64,
+                                      _i64, _i64, _i64, _c_void_p]),
+    "tl_indexer_bf16_topk": (_int, [_c_void_p, _c_void_p, _c_void_p, ctypes.c_float, _c_void_p, _i64, _i64,
+                                    _i64, _i64, _i64, _i64, _c_void_p, _c_void_p, _size, _c_void_p]),
     "tl_ki_cache_write": (_int, [_c_void_p, _i64, _c_void_p, _i64, _i64, _int, _c_void_p]),
     "tl_layernorm_rope_rotate": (_int, [_c_void_p, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p,
                                         _c_void_p, ctypes.c_float, _c_void_p]),

@@ -10,6 +10,8 @@
 // v_mfma_f32_16x16x128_f8f6f4 -- one MFMA is a whole 128-long dot product for 16 heads x
 // 16 keys.  Epilogue per MFMA: ReLU (one integer max) and the head weight (one FMA) into a
 // per-lane partial over the lane's 4 heads of each query tile.
+#include <type_traits>
+
 #include "common.h"
 #include "../../include/tilert_amd.h"
 
@@ -35,6 +37,10 @@ constexpr int kKiPageKeys = 64;
 constexpr int kKiPageBytes = kKiPageKeys * 128 + kKiPageKeys * 4;  // 8448
 
 
+// Key formats: fp8 e4m3fn keys with a per-key fp32 scale, flat ([L, 128] + [L]) or in KI
+// pages; or bf16 keys [L, 128] with no scale (the reference op's own index cache).
+enum KeyFmt { kKeyFp8 = 0, kKeyFp8Paged = 1, kKeyBf16 = 2 };
+
 // Work split.  A workgroup owns KW key ranges of NTR contiguous key tiles; SPLIT waves
 // share each range (wave sp of a range holds query tiles 4 sp .. 4 sp + 3), so the
 // range's key tiles go through LDS once for all of them.  All global loads are requested
@@ -47,30 +53,44 @@ constexpr int kKiPageBytes = kKiPageKeys * 128 + kKiPageKeys * 4;  // 8448
 // and one v_permlane16_swap leave lane l with the total of key 16 (l / 16) + l % 16 of
 // the quad (3 swaps and 3 adds per quad instead of 2 + 2 per tile), so each lane scales,
 // masks and stores one score: one 256-byte contiguous store per wave, token and quad.
-template <int M, int H, int NTR>
+// bf16 keys: a 16-key tile is 4 KB (rows of 256 B) and a (query tile, key tile) product
+// is four v_mfma_f32_16x16x32_bf16 (lane group g holds dims 32 g .. 32 g + 31 of its row,
+// step u the 8 dims 32 g + 8 u ..; queries and keys use the same assignment, so each dim
+// meets its partner exactly once).
+template <int M, int H, int NTR, int KF>
 struct IdxShape {
-  static constexpr int TPT = H / 16;                   // query tiles per token
-  static constexpr int QT = M * TPT;                   // query tiles
-  static constexpr int TW = 4 / TPT;                   // tokens per wave (4 tile slots)
-  static constexpr int SPLIT = (QT + 3) / 4;           // waves per key range
+  static constexpr bool BF16 = KF == kKeyBf16;
+  static constexpr int TB = BF16 ? 4096 : 2048;        // bytes of a 16-row tile (keys or queries)
+  static constexpr int ROWB = TB / 16;                  // bytes of one row
+  static constexpr int PIECES = ROWB / 16;              // 16-byte pieces per row
+  static constexpr int CPTILE = TB / 16;                // 16-byte pieces per tile
+  static constexpr int TPT = H / 16;                    // query tiles per token
+  static constexpr int QT = M * TPT;                    // query tiles
+  static constexpr int TW = 4 / TPT;                    // tokens per wave (4 tile slots)
+  static constexpr int SPLIT = (QT + 3) / 4;            // waves per key range
   static constexpr int KW = SPLIT >= 4 ? 1 : 4 / SPLIT;  // key ranges per workgroup
   static constexpr int WAVES = SPLIT * KW;
   static constexpr int THREADS = WAVES * 64;
-  static constexpr int NQ = NTR / 4;                   // quads per range
-  static constexpr int NT = KW * NTR;                  // key tiles per workgroup
-  static constexpr int QCH = KW * 4 * 128;             // 16-byte key chunks per quad step
+  static constexpr int NQ = NTR / 4;                    // quads per range
+  static constexpr int NT = KW * NTR;                   // key tiles per workgroup
+  static constexpr int QCH = KW * 4 * CPTILE;           // 16-byte key pieces per quad step
   static constexpr int CPT = (QCH + THREADS - 1) / THREADS;
-  static constexpr int LDS = NT * 2048 + 2048;         // + a dump row for padding chunks
-  static_assert(NTR % 4 == 0 && TPT * TW == 4, "shape");
+  static constexpr int LDS = NT * TB + 2048;            // + a dump row for padding pieces
+  static_assert(NTR % 4 == 0 && TPT * TW == 4 && WAVES <= 4, "shape");
 };
 
-template <int M, int H, int NTR, bool PAGED>
-__global__ __launch_bounds__(256) void indexer_kernel(
-    const uint8_t* __restrict__ q, const float* __restrict__ q_s, int q_s_per_head,
-    const uint8_t* __restrict__ k, const float* __restrict__ k_s, const uint16_t* __restrict__ w,
-    float* __restrict__ logits, int L, int64_t ld, int64_t cur_pos, int n_tiles) {
-  using S = IdxShape<M, H, NTR>;
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+// The indexer's scoring for one workgroup: every (token, key) of its key tiles gets
+// logits[tok, key] = ksv * sum_h wq[tok, h] * ReLU(q[tok, h] . k[key]) (ksv the key's scale
+// for fp8 keys, `kscale` for bf16 ones; wq = w * q_s), -inf past the token's position.
+template <int M, int H, int NTR, int KF>
+__device__ __forceinline__ void indexer_body(const uint8_t* __restrict__ q, const float* __restrict__ q_s,
+                                             int q_s_per_head, const uint8_t* __restrict__ k,
+                                             const float* __restrict__ k_s, const uint16_t* __restrict__ w,
+                                             float kscale, float* __restrict__ logits, int L, int64_t ld,
+                                             int64_t cur_pos, int n_tiles, uint8_t* smem) {
+  using S = IdxShape<M, H, NTR, KF>;
+  constexpr bool PAGED = KF == kKeyFp8Paged;
+  constexpr bool BF16 = S::BF16;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -84,49 +104,63 @@ __global__ __launch_bounds__(256) void indexer_kernel(
   //      offset; records past the end read as zero, so no lane clamps its address.
   //      All are unconditional and issued before any result is used, so the only waits
   //      are the compiler's in-order counts for the operands of each step.
-  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(q), 0, S::QT * 2048, kBufWord3);
-  v8i qa[4];
+  const __amdgpu_buffer_rsrc_t qrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(q), 0, S::QT * S::TB, kBufWord3);
+  v8i qa[4];      // fp8: a query tile's 128 dims in one MFMA operand
+  v8bf qb[4][4];  // bf16: four 32-dim steps
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int qt = min(4 * sp + j, S::QT - 1);
-    const int qo = (qt * 16 + r) * 128 + g * 16;
-    const u32x4v lo = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo, 0, 0);
-    const u32x4v hi = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo + 64, 0, 0);
-    qa[j] = v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
-                static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+    if constexpr (BF16) {
+      const int qo = (qt * 16 + r) * 256 + g * 64;
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        qb[j][u] = __builtin_bit_cast(v8bf, __builtin_amdgcn_raw_buffer_load_b128(qrs, qo + 16 * u, 0, 0));
+    } else {
+      const int qo = (qt * 16 + r) * 128 + g * 16;
+      const u32x4v lo = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo, 0, 0);
+      const u32x4v hi = __builtin_amdgcn_raw_buffer_load_b128(qrs, qo + 64, 0, 0);
+      qa[j] = v8i{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+                  static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+    }
   }
   // head weights and query scales of the wave's 64 (token, head) rows: one load each per
   // lane (lane l holds row 64 sp + l), spread to the MFMA layout by lane shuffles later
   const int hrow = min(64 * sp + lane, S::QT * 16 - 1);
   const uint16_t wraw = w[hrow];
-  const float qsraw = q_s[q_s_per_head ? hrow : hrow / H];
+  const float qsraw = BF16 ? 1.0f : q_s[q_s_per_head ? hrow : hrow / H];
   // key bytes of this workgroup: flat from tile wg_tile, paged from page wg_tile / 4
   // (NTR % 4 == 0, so a workgroup starts on a page); a quad of 4 tiles is one page
-  const int64_t kbase = PAGED ? static_cast<int64_t>(wg_tile / 4) * kKiPageBytes : static_cast<int64_t>(wg_tile) * 2048;
-  const int64_t kend = PAGED ? cdiv(n_tiles, 4) * kKiPageBytes : static_cast<int64_t>(L) * kBlock;
+  const int64_t kbase = PAGED ? static_cast<int64_t>(wg_tile / 4) * kKiPageBytes : static_cast<int64_t>(wg_tile) * S::TB;
+  const int64_t kend = PAGED ? cdiv(n_tiles, 4) * kKiPageBytes : static_cast<int64_t>(L) * S::ROWB;
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(k) + kbase, 0, clamp_records(kend - kbase), kBufWord3);
-  const __amdgpu_buffer_rsrc_t srs = PAGED ? krs
-      : __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(k_s) + wg_tile * 16, 0,
-                                          clamp_records((static_cast<int64_t>(L) - wg_tile * 16) * 4), kBufWord3);
-  auto tile_off = [](int lt) { return PAGED ? (lt >> 2) * kKiPageBytes + (lt & 3) * 2048 : lt * 2048; };
+  auto tile_off = [](int lt) { return PAGED ? (lt >> 2) * kKiPageBytes + (lt & 3) * 2048 : lt * S::TB; };
   float ksv[S::NQ];  // key r_tile * 16 + 64 s + lane
+  if constexpr (BF16) {
 #pragma unroll
-  for (int s = 0; s < S::NQ; ++s) {
-    const int lt = rr * NTR + 4 * s;  // workgroup-local first tile of the quad
-    ksv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-        srs, PAGED ? (lt >> 2) * kKiPageBytes + kKiPageKeys * 128 + lane * 4 : (lt * 16 + lane) * 4, 0, 0));
+    for (int s = 0; s < S::NQ; ++s) ksv[s] = kscale;
+  } else {
+    const __amdgpu_buffer_rsrc_t srs = PAGED ? krs
+        : __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(k_s) + wg_tile * 16, 0,
+                                            clamp_records((static_cast<int64_t>(L) - wg_tile * 16) * 4), kBufWord3);
+#pragma unroll
+    for (int s = 0; s < S::NQ; ++s) {
+      const int lt = rr * NTR + 4 * s;  // workgroup-local first tile of the quad
+      ksv[s] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+          srs, PAGED ? (lt >> 2) * kKiPageBytes + kKiPageKeys * 128 + lane * 4 : (lt * 16 + lane) * 4, 0, 0));
+    }
   }
-  // ---- key quads: chunk c of step s -> range c / 512, tile 4 s + (c / 128) % 4, row
-  //      (c / 8) % 16, 16-byte piece c % 8 (contiguous 1 KB reads)
+  // ---- key quads: piece c of step s -> range c / (4 CPTILE), tile 4 s + (c / CPTILE) % 4,
+  //      byte (c % CPTILE) * 16 of the tile (contiguous reads)
   u32x4v kv[S::NQ][S::CPT];
 #pragma unroll
   for (int s = 0; s < S::NQ; ++s)
 #pragma unroll
     for (int u = 0; u < S::CPT; ++u) {
       const int c = min(tid + u * S::THREADS, S::QCH - 1);
-      const int lt = (c >> 9) * NTR + 4 * s + ((c >> 7) & 3);
-      kv[s][u] = __builtin_amdgcn_raw_buffer_load_b128(krs, tile_off(lt) + (c & 127) * 16, 0, kBufNonTemporal);
+      const int lt = (c / (4 * S::CPTILE)) * NTR + 4 * s + ((c / S::CPTILE) & 3);
+      kv[s][u] = __builtin_amdgcn_raw_buffer_load_b128(krs, tile_off(lt) + (c % S::CPTILE) * 16, 0, kBufNonTemporal);
     }
   // scheduling boundary: nothing below (which waits for loads) moves above the requests
   asm volatile("" ::: "memory");
@@ -137,32 +171,48 @@ __global__ __launch_bounds__(256) void indexer_kernel(
   for (int j = 0; j < 4; ++j)
     wq[j] = make_float4(__shfl(wqv, 16 * j + 4 * g), __shfl(wqv, 16 * j + 4 * g + 1), __shfl(wqv, 16 * j + 4 * g + 2),
                         __shfl(wqv, 16 * j + 4 * g + 3));
+  if constexpr (!BF16) {
 #pragma unroll
-  for (int s = 0; s < S::NQ; ++s) asm volatile("" : "+v"(ksv[s]));  // keep the scale loads up front
+    for (int s = 0; s < S::NQ; ++s) asm volatile("" : "+v"(ksv[s]));  // keep the scale loads up front
+  }
 
   const int tok0 = (4 * sp) / S::TPT;  // first token of this wave
-  // put quad s into LDS (piece c of row r stored at piece c ^ (r & 7): conflict-free
+  // put quad s into LDS (piece c of row r stored at piece c ^ (r % PIECES): conflict-free
   // MFMA-layout reads)
   auto put = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < S::CPT; ++u) {
       const int c = tid + u * S::THREADS;
-      const int row = (c >> 3) & 15, ch = c & 7;
-      const int lt = (c >> 9) * NTR + 4 * s + ((c >> 7) & 3);  // workgroup-local tile
-      uint8_t* dst = c < S::QCH ? smem + lt * 2048 + row * 128 + ((ch ^ (row & 7)) << 4) : smem + S::NT * 2048;
+      const int row = (c / S::PIECES) & 15, ch = c % S::PIECES;
+      const int lt = (c / (4 * S::CPTILE)) * NTR + 4 * s + ((c / S::CPTILE) & 3);  // workgroup-local tile
+      uint8_t* dst = c < S::QCH ? smem + lt * S::TB + row * S::ROWB + ((ch ^ (row & (S::PIECES - 1))) << 4)
+                                : smem + S::NT * S::TB;
       *reinterpret_cast<u32x4v*>(dst) = kv[s][u];
     }
   };
   auto products = [&](int s, v4f (&c)[4][4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint8_t* tile = smem + (rr * NTR + 4 * s + i) * 2048 + r * 128;
-      const uint4 lo = *reinterpret_cast<const uint4*>(tile + ((g ^ (r & 7)) << 4));
-      const uint4 hi = *reinterpret_cast<const uint4*>(tile + (((g + 4) ^ (r & 7)) << 4));
-      const v8i kt = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
-                      static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+      const uint8_t* tile = smem + (rr * NTR + 4 * s + i) * S::TB + r * S::ROWB;
+      if constexpr (BF16) {
+        v8bf kt[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) c[i][j] = mfma_16x16x128_fp8(qa[j], kt);
+        for (int u = 0; u < 4; ++u) kt[u] = *reinterpret_cast<const v8bf*>(tile + (((4 * g + u) ^ r) << 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qb[j][u], kt[u], acc, 0, 0, 0);
+          c[i][j] = acc;
+        }
+      } else {
+        const uint4 lo = *reinterpret_cast<const uint4*>(tile + ((g ^ (r & 7)) << 4));
+        const uint4 hi = *reinterpret_cast<const uint4*>(tile + (((g + 4) ^ (r & 7)) << 4));
+        const v8i kt = {static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
+                        static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[i][j] = mfma_16x16x128_fp8(qa[j], kt);
+      }
     }
   };
   auto epilogue = [&](int s, const v4f (&c)[4][4]) __attribute__((always_inline)) {
@@ -204,21 +254,43 @@ __global__ __launch_bounds__(256) void indexer_kernel(
       }
     }
   };
-  // software pipeline: quad s + 1's MFMAs are issued before quad s's epilogue, so the
-  // matrix core works while the VALU finishes the previous quad
-  v4f cb[2][4][4];
-  put(0);
-  __syncthreads();
-  products(0, cb[0]);
+  if constexpr (BF16) {
+    // one accumulator set (the bf16 operands take the registers of the second): each
+    // quad's epilogue overlaps the other wave of the SIMD instead
+    v4f cb[4][4];
 #pragma unroll
-  for (int s = 0; s < S::NQ; ++s) {
-    if (s + 1 < S::NQ) {
-      put(s + 1);
+    for (int s = 0; s < S::NQ; ++s) {
+      put(s);
       __syncthreads();
-      products(s + 1, cb[(s + 1) & 1]);
+      products(s, cb);
+      epilogue(s, cb);
     }
-    epilogue(s, cb[s & 1]);
+  } else {
+    // software pipeline: quad s + 1's MFMAs are issued before quad s's epilogue, so the
+    // matrix core works while the VALU finishes the previous quad
+    v4f cb[2][4][4];
+    put(0);
+    __syncthreads();
+    products(0, cb[0]);
+#pragma unroll
+    for (int s = 0; s < S::NQ; ++s) {
+      if (s + 1 < S::NQ) {
+        put(s + 1);
+        __syncthreads();
+        products(s + 1, cb[(s + 1) & 1]);
+      }
+      epilogue(s, cb[s & 1]);
+    }
   }
+}
+
+template <int M, int H, int NTR, int KF>
+__global__ __launch_bounds__(256) void indexer_kernel(
+    const uint8_t* __restrict__ q, const float* __restrict__ q_s, int q_s_per_head,
+    const uint8_t* __restrict__ k, const float* __restrict__ k_s, const uint16_t* __restrict__ w, float kscale,
+    float* __restrict__ logits, int L, int64_t ld, int64_t cur_pos, int n_tiles) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  indexer_body<M, H, NTR, KF>(q, q_s, q_s_per_head, k, k_s, w, kscale, logits, L, ld, cur_pos, n_tiles, smem);
 }
 
 // Columns no token can see (key > cur_pos + M - 1) are -inf for every row.
@@ -230,70 +302,98 @@ __global__ void fill_masked_kernel(float* __restrict__ logits, int M, int64_t ld
   logits[t * ld + c] = -__builtin_inff();
 }
 
-
-template <int M, int H, int NTR, bool PAGED>
+template <int M, int H, int NTR, int KF>
 static int launch_indexer_t(hipStream_t st, const uint8_t* q, const float* q_s, int per_head, const uint8_t* k,
-                            const float* k_s, const uint16_t* w, float* logits, int L, int64_t ld, int64_t cur_pos,
-                            int n_tiles) {
-  using S = IdxShape<M, H, NTR>;
-  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, NTR, PAGED>);
-  if (S::LDS > 64 * 1024) {
-    const int rc = allow_dynamic_lds(fn, S::LDS, "indexer");
-    if (rc) return rc;
-  }
+                            const float* k_s, const uint16_t* w, float kscale, float* logits, int L, int64_t ld,
+                            int64_t cur_pos, int n_tiles) {
+  using S = IdxShape<M, H, NTR, KF>;
   const dim3 grid(static_cast<unsigned>(cdiv(n_tiles, static_cast<int64_t>(S::NT))));
-  hipLaunchKernelGGL((indexer_kernel<M, H, NTR, PAGED>), grid, dim3(S::THREADS), S::LDS, st, q, q_s, per_head, k, k_s,
-                     w, logits, L, ld, cur_pos, n_tiles);
+  const void* fn = reinterpret_cast<const void*>(indexer_kernel<M, H, NTR, KF>);
+  if (S::LDS > 64 * 1024) {
+    if (int rc = allow_dynamic_lds(fn, S::LDS, "indexer")) return rc;
+  }
+  hipLaunchKernelGGL((indexer_kernel<M, H, NTR, KF>), grid, dim3(S::THREADS), S::LDS, st, q, q_s, per_head, k, k_s, w,
+                     kscale, logits, L, ld, cur_pos, n_tiles);
   return check_launch("indexer");
 }
 
 // Key tiles per range: 16 (4 quads; two 4-wave workgroups per CU at M = 4, H = 64 --
 // measured against 8 and 32 at 128K keys: 8.0 vs 8.4 / 8.4 us) while that still gives
 // >= 512 workgroups, fewer for short caches so the grid keeps filling the chip.
-template <int M, int H, bool PAGED>
-static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, int per_head,
-                          const uint8_t* k, const float* k_s, const uint16_t* w, float* logits,
-                          int L, int64_t ld, int64_t cur_pos, int n_tiles) {
-  constexpr int KW = IdxShape<M, H, 4>::KW;
-  int ntr = 16;
+template <int M, int H, int KF>
+static int launch_indexer(hipStream_t st, const uint8_t* q, const float* q_s, int per_head, const uint8_t* k,
+                          const float* k_s, const uint16_t* w, float kscale, float* logits, int L, int64_t ld,
+                          int64_t cur_pos, int n_tiles) {
+  constexpr int KW = IdxShape<M, H, 4, KF>::KW;
+  // bf16 keys: at most 16 tiles per workgroup (66 KB of LDS, 64 prefetch registers)
+  constexpr int kMaxNtr = KF == kKeyBf16 ? (16 / KW < 4 ? 4 : 16 / KW) : 16;
+  int ntr = kMaxNtr;
   while (ntr > 4 && cdiv(n_tiles, static_cast<int64_t>(KW) * ntr) < 512) ntr /= 2;
-  switch (ntr) {
-    case 4: return launch_indexer_t<M, H, 4, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    case 8: return launch_indexer_t<M, H, 8, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
-    default: return launch_indexer_t<M, H, 16, PAGED>(st, q, q_s, per_head, k, k_s, w, logits, L, ld, cur_pos, n_tiles);
+  auto run = [&](auto ntr_tag) {
+    constexpr int NTR = decltype(ntr_tag)::value;
+    return launch_indexer_t<M, H, NTR, KF>(st, q, q_s, per_head, k, k_s, w, kscale, logits, L, ld, cur_pos, n_tiles);
+  };
+  if constexpr (kMaxNtr >= 16) {
+    if (ntr == 16) return run(std::integral_constant<int, 16>{});
   }
+  if constexpr (kMaxNtr >= 8) {
+    if (ntr == 8) return run(std::integral_constant<int, 8>{});
+  }
+  return run(std::integral_constant<int, 4>{});
 }
 
-template <bool PAGED>
-static int indexer_scores(const char* who, const void* q_fp8, const float* q_s, int q_s_per_head, const void* k_fp8,
-                          const float* k_s, const void* w_bf16, float* logits, int64_t M, int64_t H, int64_t L,
-                          int64_t ld, int64_t cur_pos, void* stream) {
+// Shared argument checks and dispatch of every indexer entry point.  topk > 0 adds the
+// exact top-k (indices int32 [M, topk] into `out`): tl_topk_rows on the logits just written,
+// on the same stream, with the caller's workspace (tl_indexer_topk_workspace_bytes).
+// Measured and not kept: the selection fused into the scoring launch (see the top-k notes of
+// the package documentation) -- every variant was slower than the two launches.
+template <int KF>
+static int indexer_run(const char* who, const void* q, const float* q_s, int q_s_per_head, const void* kp,
+                       const float* k_s, const void* w_bf16, float kscale, float* logits, int64_t M, int64_t H,
+                       int64_t L, int64_t ld, int64_t cur_pos, int64_t topk, int32_t* out, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  constexpr bool BF16 = KF == kKeyBf16;
   if (H != 32 && H != 64) { set_error("%s: H=%lld must be 32 or 64", who, (long long)H); return kErrUnsupported; }
   if (M < 1 || M * H > 256) { set_error("%s: need 1 <= M and M*H <= 256 (M=%lld H=%lld)", who, (long long)M, (long long)H); return kErrUnsupported; }
   if (L < 0 || L > (1ll << 28) || ld < L) { set_error("%s: bad L=%lld / ld=%lld", who, (long long)L, (long long)ld); return kErrArg; }
   if (cur_pos < 0) { set_error("%s: cur_pos=%lld must be >= 0", who, (long long)cur_pos); return kErrArg; }
-  if (!q_fp8 || !q_s || !k_fp8 || (!PAGED && !k_s) || !w_bf16 || !logits) { set_error("%s: null pointer", who); return kErrArg; }
-  if ((reinterpret_cast<uintptr_t>(q_fp8) | reinterpret_cast<uintptr_t>(k_fp8)) & 15) { set_error("%s: q and k must be 16-byte aligned", who); return kErrArg; }
-  if (L == 0) return kOk;
+  if (!q || (!BF16 && !q_s) || !kp || (KF == kKeyFp8 && !k_s) || !w_bf16 || !logits) { set_error("%s: null pointer", who); return kErrArg; }
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kp)) & 15) { set_error("%s: q and k must be 16-byte aligned", who); return kErrArg; }
+  if (topk > 0) {
+    // validated before anything is launched (tl_topk_rows repeats these checks)
+    if (L == 0) { set_error("%s: top-k over an empty cache", who); return kErrArg; }
+    const size_t need = tl_topk_workspace_bytes(M, ld, topk);
+    if (need == 0 || topk > 8192 || ld % 4 || (reinterpret_cast<uintptr_t>(logits) & 15)) {
+      set_error("%s: top-k needs topk <= 8192, ld %% 4 == 0, 16-byte aligned logits and ld <= 262144", who);
+      return kErrUnsupported;
+    }
+    if (!out) { set_error("%s: null indices", who); return kErrArg; }
+    if (!workspace || workspace_bytes < need) { set_error("%s: workspace of %zu bytes required (got %zu)", who, need, workspace_bytes); return kErrArg; }
+  }
   hipStream_t st = (hipStream_t)stream;
   // keys past the last token's position are masked for every token: no need to read them
   const int64_t visible = cur_pos + M < L ? cur_pos + M : L;
-  const int n_tiles = static_cast<int>(cdiv(visible, 16));
   if (visible < L) {
     const int64_t n = (L - visible) * M;
     hipLaunchKernelGGL(fill_masked_kernel, dim3(cdiv(n, 256)), dim3(256), 0, st, logits, (int)M, ld, visible, L);
   }
-  const uint8_t* q = (const uint8_t*)q_fp8;
-  const uint8_t* k = (const uint8_t*)k_fp8;
-  const uint16_t* w = (const uint16_t*)w_bf16;
-  const int Li = static_cast<int>(L);
+  int rc = kOk;
+  if (visible > 0) {
+    const int n_tiles = static_cast<int>(cdiv(visible, 16));
+    const uint8_t* qq = (const uint8_t*)q;
+    const uint8_t* k = (const uint8_t*)kp;
+    const uint16_t* w = (const uint16_t*)w_bf16;
+    const int Li = static_cast<int>(L);
+    rc = kErrUnsupported;
 #define TL_IDX(MM, HH) \
-  if (M == MM && H == HH) return launch_indexer<MM, HH, PAGED>(st, q, q_s, q_s_per_head, k, k_s, w, logits, Li, ld, cur_pos, n_tiles);
-  TL_IDX(1, 64) TL_IDX(2, 64) TL_IDX(3, 64) TL_IDX(4, 64)
-  TL_IDX(1, 32) TL_IDX(2, 32) TL_IDX(3, 32) TL_IDX(4, 32) TL_IDX(5, 32) TL_IDX(6, 32) TL_IDX(7, 32) TL_IDX(8, 32)
+    if (M == MM && H == HH) rc = launch_indexer<MM, HH, KF>(st, qq, q_s, q_s_per_head, k, k_s, w, kscale, logits, Li, ld, cur_pos, n_tiles);
+    TL_IDX(1, 64) TL_IDX(2, 64) TL_IDX(3, 64) TL_IDX(4, 64)
+    TL_IDX(1, 32) TL_IDX(2, 32) TL_IDX(3, 32) TL_IDX(4, 32) TL_IDX(5, 32) TL_IDX(6, 32) TL_IDX(7, 32) TL_IDX(8, 32)
 #undef TL_IDX
-  set_error("%s: unsupported M=%lld H=%lld", who, (long long)M, (long long)H);
-  return kErrUnsupported;
+    if (rc == kErrUnsupported) set_error("%s: unsupported M=%lld H=%lld", who, (long long)M, (long long)H);
+  }
+  if (rc != kOk || topk <= 0) return rc;
+  return tl_topk_rows(logits, M, ld, cur_pos, topk, out, workspace, workspace_bytes, stream);
 }
 
 // One thread per 8 key elements, 16 threads per key: quantise the key like act_quant
@@ -420,8 +520,8 @@ extern "C" int tl_indexer_fp8_scores(const void* q_fp8, const float* q_s, int q_
                                      const void* k_fp8, const float* k_s, const void* w_bf16,
                                      float* logits, int64_t M, int64_t H, int64_t L, int64_t ld,
                                      int64_t cur_pos, void* stream) {
-  return indexer_scores<false>("indexer", q_fp8, q_s, q_s_per_head, k_fp8, k_s, w_bf16, logits, M, H, L, ld, cur_pos,
-                               stream);
+  return indexer_run<kKeyFp8>("indexer", q_fp8, q_s, q_s_per_head, k_fp8, k_s, w_bf16, 1.0f, logits, M, H, L, ld,
+                              cur_pos, 0, nullptr, nullptr, 0, stream);
 }
 
 extern "C" int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, int q_s_per_head,
@@ -432,8 +532,37 @@ extern "C" int tl_indexer_fp8_scores_paged(const void* q_fp8, const float* q_s, 
     set_error("indexer_paged: L=%lld keys need %lld pages (got %lld)", (long long)L, (long long)cdiv(L, kKiPageKeys), (long long)n_pages);
     return kErrArg;
   }
-  return indexer_scores<true>("indexer_paged", q_fp8, q_s, q_s_per_head, ki_pages, nullptr, w_bf16, logits, M, H, L, ld,
-                              cur_pos, stream);
+  return indexer_run<kKeyFp8Paged>("indexer_paged", q_fp8, q_s, q_s_per_head, ki_pages, nullptr, w_bf16, 1.0f, logits,
+                                   M, H, L, ld, cur_pos, 0, nullptr, nullptr, 0, stream);
+}
+
+extern "C" size_t tl_indexer_topk_workspace_bytes(int64_t M, int64_t ld, int64_t topk) {
+  return tl_topk_workspace_bytes(M, ld, topk);
+}
+
+extern "C" int tl_indexer_fp8_topk(const void* q_fp8, const float* q_s, int q_s_per_head, const void* k_fp8,
+                                   const float* k_s, const void* w_bf16, float* logits, int64_t M, int64_t H,
+                                   int64_t L, int64_t ld, int64_t cur_pos, int64_t topk, int32_t* indices,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (topk < 1) { set_error("indexer_topk: topk=%lld must be positive", (long long)topk); return kErrArg; }
+  return indexer_run<kKeyFp8>("indexer_topk", q_fp8, q_s, q_s_per_head, k_fp8, k_s, w_bf16, 1.0f, logits, M, H, L, ld,
+                              cur_pos, topk, indices, workspace, workspace_bytes, stream);
+}
+
+extern "C" int tl_indexer_bf16_scores(const void* q_bf16, const void* k_bf16, const void* w_bf16, float score_scale,
+                                      float* logits, int64_t M, int64_t H, int64_t L, int64_t ld, int64_t cur_pos,
+                                      void* stream) {
+  return indexer_run<kKeyBf16>("indexer_bf16", q_bf16, nullptr, 0, k_bf16, nullptr, w_bf16, score_scale, logits, M, H,
+                               L, ld, cur_pos, 0, nullptr, nullptr, 0, stream);
+}
+
+extern "C" int tl_indexer_bf16_topk(const void* q_bf16, const void* k_bf16, const void* w_bf16, float score_scale,
+                                    float* logits, int64_t M, int64_t H, int64_t L, int64_t ld, int64_t cur_pos,
+                                    int64_t topk, int32_t* indices, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  if (topk < 1) { set_error("indexer_bf16_topk: topk=%lld must be positive", (long long)topk); return kErrArg; }
+  return indexer_run<kKeyBf16>("indexer_bf16_topk", q_bf16, nullptr, 0, k_bf16, nullptr, w_bf16, score_scale, logits, M,
+                               H, L, ld, cur_pos, topk, indices, workspace, workspace_bytes, stream);
 }
 
 extern "C" int tl_ki_cache_write(const void* k_bf16, int64_t rows, void* ki_pages, int64_t n_pages, int64_t pos,
