@@ -134,7 +134,10 @@ int tl_fp8_gemm_packed(const void* a, const float* a_s, const void* b_packed, co
  * exceed the maximum fail with status 3 (every dense MLP shape of 7168 <-> 18432 up to
  * M = 256 fits).  Every call on a GPU shares that GPU's array: calls that overlap on one GPU
  * (different streams, or different threads without ordering) race; calls on one stream are
- * safe.  A device's first call enqueues a small fill kernel that zeroes the counters. */
+ * safe.  The array is zero when the library's code object loads and every call leaves its
+ * counters zero again, so no call clears it (a first call may be made under graph
+ * capture).  The 40 MiB are reserved on every GPU where the library's code object is
+ * loaded, whether or not this entry point is called. */
 #define TL_FP8_GEMM_STATIC_SCRATCH_BYTES (40u << 20)
 int tl_fp8_gemm_packed_static(const void* a, const float* a_s, const void* b_packed, const float* b_s,
                               void* c_bf16, int64_t M, int64_t N, int64_t K, void* stream);

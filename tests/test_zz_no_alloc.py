@@ -43,7 +43,7 @@ def _static(xq, xs, packed, M, N, Kd, dev):
 
 
 @pytest.mark.parametrize("first,second", [
-    # stream-K MFMA GEMM (partials + image), then the split-K GEMV over its leftovers
+    # the wide MFMA GEMM with a K split (fp32 partials), then the split-K GEMV over its leftovers
     ((256, 7168, 4096), (40, 576, 7168)),
     # GEMV with the activation image and 4 row tiles, then a plain M = 4 GEMV (no scratch)
     ((64, 18432, 7168), (4, 1024, 2048)),

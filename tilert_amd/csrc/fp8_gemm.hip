@@ -1394,15 +1394,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};  // device address of each device's `scratch`
 
-__global__ void zero_words_kernel(uint32_t* __restrict__ p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0u;
-}
-
-// The current device's scratch address; on a device's first call it is looked up and the
-// counter region (which every call leaves zero again) is cleared with a fill kernel on
-// `st`, ahead of that call's GEMM.
-int scratch_for_current_device(hipStream_t st, void** out) {
+// The current device's scratch address, looked up on the device's first call.  The array
+// is zero-initialised when the code object is loaded (device globals have static storage),
+// and every call leaves its counter region zero again, so no call needs to clear it: two
+// threads making their first calls on different streams cannot see an uncleared array, and
+// a first call made under graph capture records nothing extra.
+int scratch_for_current_device(void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) { set_error("fp8_gemm_packed_static: hipGetDevice failed: %s", hipGetErrorString(e)); return kErrHip; }
@@ -1415,9 +1412,6 @@ int scratch_for_current_device(hipStream_t st, void** out) {
       set_error("fp8_gemm_packed_static: hipGetSymbolAddress failed on device %d: %s", dev, hipGetErrorString(e));
       return kErrHip;
     }
-    const int words = static_cast<int>(kCounterBytes / sizeof(uint32_t));
-    hipLaunchKernelGGL(zero_words_kernel, dim3(cdiv(words, 256)), dim3(256), 0, st, static_cast<uint32_t*>(ptr), words);
-    if (int rc = check_launch("fp8_gemm_packed_static")) return rc;
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -1440,7 +1434,7 @@ extern "C" int tl_fp8_gemm_packed_static(const void* a, const float* a_s, const 
   }
   void* ws = nullptr;
   if (need) {
-    rc = scratch_for_current_device((hipStream_t)stream, &ws);
+    rc = scratch_for_current_device(&ws);
     if (rc) return rc;
   }
   return launch_gemm<true>((const uint8_t*)a, a_s, (const uint8_t*)b_packed, b_s, plain_out((uint16_t*)c_bf16, (int)N),
