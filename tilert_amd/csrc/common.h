@@ -180,19 +180,22 @@ __device__ inline void copy_to_lds4(const void* src, uint8_t* lds) {
 // every i, so the steady-state loop has a fixed number of loads in flight and the
 // compiler's wait counts cover only the operands being consumed.  Buffer indices are
 // compile-time constants (the loop is unrolled by D), so no register copies -- which
-// would wait for the loads -- are needed.  The last 2D-2 items run in a guarded tail.
+// would wait for the loads -- are needed.  The last 2D-2 items run in a guarded tail; a
+// stream of fewer than D-1 items issues all its loads, runs start(), then computes them
+// (no round trip per item).
 // start() runs once, after the first fetches are issued and before the first compute
 // (for work that should overlap them, e.g. filling LDS); it runs even when n == 0, so it
 // may contain a workgroup barrier as long as every wave calls ring_pipeline.
 template <int D, class Buf, class Fetch, class Compute, class Start>
 __device__ inline void ring_pipeline(int n, Buf (&buf)[D], Fetch&& fetch, Compute&& compute, Start&& start) {
-  if (n < D - 1) {  // too short to fill the ring
-    if (n > 0) fetch(0, buf[0]);
+  if (n < D - 1) {  // too short to fill the ring: every item's loads are issued up front
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (j < n) fetch(j, buf[j]);
     start();
-    for (int i = 0; i < n; ++i) {
-      if (i > 0) fetch(i, buf[0]);
-      compute(i, buf[0]);
-    }
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (j < n) compute(j, buf[j]);
     return;
   }
 #pragma unroll

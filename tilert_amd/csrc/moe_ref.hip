@@ -44,7 +44,8 @@ constexpr int kRefMaskWords = 5;            // local experts < 320 (shared + 256
 constexpr int kRefMaxLocal = 64 * kRefMaskWords;
 constexpr int kRefMaxRouted = 256;          // 4 per lane in the routing wave
 constexpr int kRefLdsX = 64 * 1024;         // staged activations (x or gathered h)
-constexpr int kRefDepth = 2;                // weight blocks in flight per wave
+constexpr int kRefGuDepth = 2;              // gate/up weight blocks (2 fragments each) in flight per wave
+constexpr int kRefDnDepth = 6;              // down weight fragments in flight per wave
 
 // Hit set over local experts, wave-uniform (scalar registers).
 struct ExpertMask {
@@ -125,9 +126,42 @@ __device__ inline int token_pos(int pe, float pw, int P, int r, int e, float& w)
   return pos;
 }
 
+// fp32 sum over the wave by DPP (row shifts, then row broadcasts; lane 63 ends with it).
+__device__ inline float wave_sum_f32(float v) {
+#define TL_DPP_ADD(ctrl, rmask) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xf, false))
+  TL_DPP_ADD(0x111, 0xf);
+  TL_DPP_ADD(0x112, 0xf);
+  TL_DPP_ADD(0x114, 0xf);
+  TL_DPP_ADD(0x118, 0xf);
+  TL_DPP_ADD(0x142, 0xa);
+  TL_DPP_ADD(0x143, 0xc);
+#undef TL_DPP_ADD
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // ------------------------------------------------------------------------ routing
-// One wave per token: lane l holds routed experts l, l + 64, l + 128, l + 192.
+// One wave per token: lane l holds routed experts l, l + 64, l + 128, l + 192.  The wave
+// is latency-bound (one wave, dependent steps), so every reduction is a register-level one:
+// groups of 32 experts (DeepSeek-V3.2's 8 groups of 256) are the two 32-lane halves of one
+// expert column, reduced with xor shuffles; each top-k round is one DPP max over
+// order-preserving keys and a ballot for the lowest expert holding it.
 __device__ inline bool better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
+
+__device__ inline uint32_t route_key(float f) {  // larger float, larger key; 0 = unavailable
+  const uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Wave max by DPP (row shifts, then row broadcasts: lane 63 ends with the result).
+__device__ inline uint32_t route_wave_max(uint32_t x) {
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x111, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x112, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x114, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x118, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x142, 0xa, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x143, 0xc, 0xf, false)));
+  return __builtin_amdgcn_readlane(x, 63);
+}
 
 __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ scores, const float* __restrict__ bias,
                                                        int n, int topk, int n_groups, int topk_groups, float route_scale,
@@ -148,64 +182,92 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
   }
   if (n_groups > 1) {  // keep the topk_groups best groups (score: top-2 sum with bias, else max)
     const int gsz = n / n_groups;
+    if (gsz == 32 && n == 256) {
+      // group 2 i + (lane >= 32) is held by one 32-lane half of column i: top-2 by xor shuffles
+      float gs[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (live[i]) bl[lane + 64 * i] = b[i];
-    __syncthreads();
-    if (lane < n_groups) {
-      float m1 = -INFINITY, m2 = -INFINITY;
-      for (int j = 0; j < gsz; ++j) {
-        const float v = bl[lane * gsz + j];
-        if (v > m1) {
-          m2 = m1;
-          m1 = v;
-        } else if (v > m2) {
-          m2 = v;
+      for (int i = 0; i < 4; ++i) {
+        float m1 = b[i], m2 = -INFINITY;
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) {
+          const float o1 = __shfl_xor(m1, o), o2 = __shfl_xor(m2, o);
+          const float lo = fminf(m1, o1);
+          m1 = fmaxf(m1, o1);
+          m2 = fmaxf(lo, fmaxf(m2, o2));
         }
+        gs[i] = bias ? m1 + m2 : m1;
       }
-      gscore[lane] = bias ? m1 + m2 : m1;
-    }
-    __syncthreads();
-    if (lane < n_groups) {
-      int rank = 0;
-      for (int g = 0; g < n_groups; ++g) rank += better(gscore[g], g, gscore[lane], lane) ? 1 : 0;
-      gkeep[lane] = rank < topk_groups;
-    }
-    __syncthreads();
+      // group g's score: column g / 2, half g % 2
+      float gv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (live[i] && !gkeep[(lane + 64 * i) / gsz]) b[i] = -INFINITY;
+      for (int g = 0; g < 8; ++g) gv[g] = __shfl(gs[g >> 1], (g & 1) * 32);
+      bool keep[8];
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        int rank = 0;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) rank += better(gv[h], h, gv[g], g) ? 1 : 0;
+        keep[g] = rank < topk_groups;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool k0 = keep[2 * i], k1 = keep[2 * i + 1];
+        if (!(lane < 32 ? k0 : k1)) b[i] = -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (live[i]) bl[lane + 64 * i] = b[i];
+      __syncthreads();
+      if (lane < n_groups) {
+        float m1 = -INFINITY, m2 = -INFINITY;
+        for (int j = 0; j < gsz; ++j) {
+          const float v = bl[lane * gsz + j];
+          if (v > m1) {
+            m2 = m1;
+            m1 = v;
+          } else if (v > m2) {
+            m2 = v;
+          }
+        }
+        gscore[lane] = bias ? m1 + m2 : m1;
+      }
+      __syncthreads();
+      if (lane < n_groups) {
+        int rank = 0;
+        for (int g = 0; g < n_groups; ++g) rank += better(gscore[g], g, gscore[lane], lane) ? 1 : 0;
+        gkeep[lane] = rank < topk_groups;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (live[i] && !gkeep[(lane + 64 * i) / gsz]) b[i] = -INFINITY;
+    }
   }
-  // top-k by repeated wave arg-max (descending, lowest expert first on ties)
-  bool taken[4] = {false, false, false, false};
+  // top-k by repeated wave arg-max (descending, lowest expert first on ties); taken and
+  // absent experts hold key 0, below every float
+  uint32_t key[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) key[i] = live[i] ? route_key(b[i]) : 0u;
   int my_e = 0;
   float my_s = 0.f, sum = 0.f;
   for (int r = 0; r < topk; ++r) {
-    float bv = -INFINITY;
-    int be = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (live[i] && !taken[i] && better(b[i], lane + 64 * i, bv, be)) {
-        bv = b[i];
-        be = lane + 64 * i;
-      }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oe = __shfl_xor(be, o);
-      if (better(ov, oe, bv, be)) {
-        bv = ov;
-        be = oe;
-      }
-    }
-    const int owner = be & 63, slot = be >> 6;
+    const uint32_t kmax = route_wave_max(max(max(key[0], key[1]), max(key[2], key[3])));
+    // the lowest expert with that key: the lowest column i, then the lowest lane
+    int be = 0;
     float sv = 0.f;
+    bool found = false;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (i == slot) sv = s[i];
-      if (lane == owner && i == slot) taken[i] = true;
+      const uint64_t bal = __ballot(key[i] == kmax);
+      if (!found && bal) {
+        const int owner = __builtin_ctzll(bal);
+        be = 64 * i + owner;
+        sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s[i]), owner));
+        if (lane == owner) key[i] = 0u;
+        found = true;
+      }
     }
-    sv = __shfl(sv, owner);
     if (lane == r) {
       my_e = be;
       my_s = sv;
@@ -232,52 +294,115 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
   extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
   __shared__ float red[kRefWaves - 1][2][4][64];
   __shared__ float ssq[16][kRefWaves];
+  __shared__ int8_t ptab[64 * 16];  // [slot][token]: the position where the token uses the slot's expert, -1 none
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int pe;
   float pw;
   pair_lane<DENSE>(idx, nullptr, M, P, topk, n_local, pe, pw);
+  const ExpertMask mask = lanes_mask(pe);  // waits for the routing loads (MoE)
+  // x straight into LDS (no registers); waited for in the first item's ring start, after the
+  // first weight fetches have been requested
   const int x16 = M * D / 8;
-  stage_commit(xl, stage_issue(x, x16), x16);
-  const ExpertMask mask = lanes_mask(pe);
-  __syncthreads();
-  if (DENSE) {  // RMSNorm of the staged rows: x * (1 / sqrt(mean(x^2) + eps)) * gamma, fp32
-    const int c16 = D / 8;
-    for (int m = 0; m < M; ++m) {
-      float acc = 0.f;
-      for (int c = threadIdx.x; c < c16; c += blockDim.x) {
-        const u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float lo = bf16_to_f32(v[j] & 0xffffu), hi = bf16_to_f32(v[j] >> 16);
-          acc += lo * lo + hi * hi;
-        }
-      }
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
-      if (lane == 0) ssq[m][wave] = acc;
-    }
-    __syncthreads();
-    for (int m = 0; m < M; ++m) {
-      float ss = 0.f;
-#pragma unroll
-      for (int w = 0; w < kRefWaves; ++w) ss += ssq[m][w];
-      const float rs = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
-      for (int c = threadIdx.x; c < c16; c += blockDim.x) {
-        u32x4 v = reinterpret_cast<u32x4*>(xl + m * D)[c];
-        const v4f g0 = *reinterpret_cast<const v4f*>(gamma + 8 * c);
-        const v4f g1 = *reinterpret_cast<const v4f*>(gamma + 8 * c + 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float ga = j < 2 ? g0[2 * j] : g1[2 * j - 4], gb = j < 2 ? g0[2 * j + 1] : g1[2 * j - 3];
-          v[j] = f32_to_bf16(bf16_to_f32(v[j] & 0xffffu) * rs * ga) |
-                 (static_cast<uint32_t>(f32_to_bf16(bf16_to_f32(v[j] >> 16) * rs * gb)) << 16);
-        }
-        reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
-      }
-    }
-    __syncthreads();
+  {  // every chunk once (the copies are waited for explicitly, so their count may vary)
+    const int c0 = threadIdx.x - lane;
+    for (int cw = c0; cw < x16; cw += kRefWaves * 64)  // cw: this wave's first chunk (uniform)
+      if (cw + lane < x16)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(x) + cw + lane,
+                                         (lds_ptr)(xl + static_cast<size_t>(cw) * 8), 16, 0, 0);
   }
+  // DENSE: this thread's gamma values for the norm (its chunks c = tid, tid + 512 of a row)
+  constexpr int kNormChunks = 2;  // D / 8 <= 1024 chunks of 8 per row
+  v4f gm[kNormChunks][2];
+  if (DENSE) {
+#pragma unroll
+    for (int u = 0; u < kNormChunks; ++u) {
+      const int c = min(static_cast<int>(threadIdx.x) + u * kRefWaves * 64, D / 8 - 1);
+      gm[u][0] = *reinterpret_cast<const v4f*>(gamma + 8 * c);
+      gm[u][1] = *reinterpret_cast<const v4f*>(gamma + 8 * c + 4);
+    }
+  }
+  if (!DENSE && wave == 0) {  // position table from the lane-held pairs
+    for (int i = lane; i < 64 * 16; i += 64) ptab[i] = -1;
+    if (pe >= 0) {
+      int slot = 0;
+#pragma unroll
+      for (int k = 0; k < kRefMaskWords; ++k) {
+        const int base = 64 * k;
+        slot += __builtin_popcountll(pe >= base + 64 ? mask.w[k]
+                                                     : (pe > base ? mask.w[k] & ((1ull << (pe - base)) - 1ull) : 0ull));
+      }
+      const int t = lane / P;
+      ptab[slot * 16 + t] = static_cast<int8_t>(lane - t * P);
+    }
+  }
+  bool prepared = false;
+  // first item's ring start: x has landed; DENSE: RMSNorm of the staged rows in place,
+  // x * (1 / sqrt(mean(x^2) + eps)) * gamma in fp32, rounded to bf16 (the rows' partial sums
+  // reduced together)
+  auto prepare = [&]() {
+    if (prepared) return;
+    prepared = true;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (DENSE) {
+      // every row's sum of squares at once: this thread's chunks, then one DPP wave sum per
+      // row (independent chains), then the 8 wave partials through LDS
+      const int c16 = D / 8;
+      float acc[16];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+#pragma unroll
+      for (int u = 0; u < kNormChunks; ++u) {
+        const int c = threadIdx.x + u * kRefWaves * 64;
+        if (c < c16) {
+#pragma unroll
+          for (int m = 0; m < 16; ++m) {
+            if (m < M) {
+              const u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const float lo = bf16_to_f32(v[j] & 0xffffu), hi = bf16_to_f32(v[j] >> 16);
+                acc[m] += lo * lo + hi * hi;
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        if (m < M) {
+          const float a = wave_sum_f32(acc[m]);
+          if (lane == 0) ssq[m][wave] = a;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        if (m < M) {
+          float ss = 0.f;
+#pragma unroll
+          for (int w = 0; w < kRefWaves; ++w) ss += ssq[m][w];
+          const float rs = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+          for (int u = 0; u < kNormChunks; ++u) {
+            const int c = threadIdx.x + u * kRefWaves * 64;
+            if (c < c16) {
+              u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {  // RNE to bf16 two at a time (v_cvt_pk_bf16_f32)
+                const float ga = gm[u][j >> 1][2 * (j & 1)], gb = gm[u][j >> 1][2 * (j & 1) + 1];
+                const v2f pr = {bf16_to_f32(v[j] & 0xffffu) * rs * ga, bf16_to_f32(v[j] >> 16) * rs * gb};
+                v[j] = bf16x2_bits(pr);
+              }
+              reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    }
+  };
   const int KB = D >> 7, tiles = I >> 4, rows_e = 2 * I;
   const int r = lane & 15, g = lane >> 4;
   const uint16_t* xrow = xl + min(r, M - 1) * D;
@@ -295,7 +420,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
       v8i wg, wu;
       float gs, us;
     };
-    Ops buf[kRefDepth];
+    Ops buf[kRefGuDepth];
     ring_pipeline(
         n, buf,
         [&](int i, Ops& o) {
@@ -315,7 +440,8 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
             ag = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wg[2 * j], o.wg[2 * j + 1], o.gs), xa, ag, 0, 0, 0);
             au = __builtin_amdgcn_mfma_f32_16x16x32_bf16(dequant8_bf16(o.wu[2 * j], o.wu[2 * j + 1], o.us), xa, au, 0, 0, 0);
           }
-        });
+        },
+        prepare);
     if (wave > 0) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -332,8 +458,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
           ag[j] += red[w][0][j][lane];
           au[j] += red[w][1][j][lane];
         }
-      float unused;
-      const int pos = token_pos(pe, pw, P, min(r, M - 1), e, unused);
+      const int pos = DENSE ? e : ptab[slot * 16 + min(r, M - 1)];
       if (r < M && pos >= 0) {
         uint16_t o[4];
 #pragma unroll
@@ -345,12 +470,13 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     }
     __syncthreads();
   }
+  if (!prepared) __builtin_amdgcn_s_waitcnt(0);  // no item: the LDS copies land before the workgroup ends
 }
 
 // -------------------------------------------------------------------- down + combine
 // One workgroup per 16-row output tile.  The rows each hit expert multiplies -- token r's
 // h row at the position where r uses it, zero where r does not -- are gathered into LDS as
-// [slot][M][I]; wave w takes slots w, w + 8, ... with all their K blocks (kRefDepth weight
+// [slot][M][I]; wave w takes slots w, w + 8, ... with all their K blocks (kRefGuDepth weight
 // blocks in flight), so each slot's product is complete in one wave, which then adds the
 // per-token terms bf16(weight * product) (the goldens' per-term rounding) to its fp32
 // partial.  The 8 wave partials are summed in wave order (deterministic), rounded to bf16,
@@ -360,8 +486,10 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
     const uint16_t* __restrict__ h, const uint8_t* __restrict__ w2, const float* __restrict__ s2,
     const int32_t* __restrict__ idx, const float* __restrict__ probs, const uint16_t* __restrict__ x_in, int M,
     int P, int topk, int n_local, int D, int I, uint16_t* __restrict__ y) {
-  extern __shared__ __align__(16) uint16_t hl[];  // [n_hit][M][I]
+  extern __shared__ __align__(16) uint16_t hl[];  // [M * P + 1][I]: h, then a zero row
   __shared__ float red[kRefWaves][4][64];
+  __shared__ float wtab[64 * 16];    // [slot][token]: the token's routing weight for the slot's expert (0: unused)
+  __shared__ uint8_t rtab[64 * 16];  // [slot][token]: the row of hl the product reads (MoE)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int pe;
@@ -372,20 +500,45 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
   const int r = lane & 15, g = lane >> 4;
   const int row = min(r, M - 1);
   const int rt = blockIdx.x;
-  // gather: wave w fills slots w, w + 8, ... (16-byte chunks; rows a token does not use
-  // are zero)
-  const int c_row = I / 8;
-  for (int j = wave; j < mask.n; j += kRefWaves) {
-    const int e = mask_nth(mask, j);
-    for (int t = 0; t < M; ++t) {
-      float unused;
-      const int pos = token_pos(pe, pw, P, t, e, unused);
-      const u32x4* src = reinterpret_cast<const u32x4*>(h + (static_cast<size_t>(t) * P + max(pos, 0)) * I);
-      u32x4* dst = reinterpret_cast<u32x4*>(hl + (static_cast<size_t>(j) * M + t) * I);
-      for (int c = lane; c < c_row; c += 64) dst[c] = pos >= 0 ? src[c] : u32x4{0u, 0u, 0u, 0u};
+  // The slot of this lane's pair's expert: the rank of pe in the hit set.  h ([M * P][I], pair
+  // q = token q / P, position q % P) is copied whole into LDS, followed by one zero row; the
+  // product of slot j for token t reads row rtab[j][t]: its pair's row, or the zero row when
+  // the token does not use the slot's expert.  The copy runs once the first weight fetches are
+  // in flight (ring_pipeline's start).
+  int pslot = -1;
+  if (pe >= 0) {
+    pslot = 0;
+#pragma unroll
+    for (int k = 0; k < kRefMaskWords; ++k) {
+      const int base = 64 * k;
+      const uint64_t below = pe >= base + 64 ? mask.w[k] : (pe > base ? mask.w[k] & ((1ull << (pe - base)) - 1ull) : 0ull);
+      pslot += __builtin_popcountll(below);
     }
   }
-  __syncthreads();
+  const int pairs = M * P;
+  auto gather = [&]() {
+    const int h16 = pairs * I / 8;  // 16-byte chunks of h
+    const int c0 = threadIdx.x - lane;
+    for (int cw = c0; cw < h16; cw += kRefWaves * 64)  // cw: this wave's first chunk (uniform)
+      if (cw + lane < h16)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(h) + cw + lane,
+                                         (lds_ptr)(hl + static_cast<size_t>(cw) * 8), 16, 0, 0);
+    for (int c = threadIdx.x; c < I / 8; c += blockDim.x)  // the zero row
+      reinterpret_cast<u32x4*>(hl + static_cast<size_t>(pairs) * I)[c] = u32x4{0u, 0u, 0u, 0u};
+    if (!DENSE) {
+      for (int c = threadIdx.x; c < mask.n * 16; c += blockDim.x) {
+        wtab[c] = 0.f;
+        rtab[c] = static_cast<uint8_t>(pairs);
+      }
+      __syncthreads();
+      if (wave == 0 && pslot >= 0) {  // the pair's weight (shared: 1) and row
+        wtab[pslot * 16 + lane / P] = pw;
+        rtab[pslot * 16 + lane / P] = static_cast<uint8_t>(lane);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  };
   v4f yacc = {0.f, 0.f, 0.f, 0.f};
   v4f acc = {0.f, 0.f, 0.f, 0.f};
   const int my_slots = wave < mask.n ? (mask.n - wave + kRefWaves - 1) / kRefWaves : 0;
@@ -394,7 +547,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
     v8i w;
     float sc;
   };
-  Ops buf[kRefDepth];
+  Ops buf[kRefDnDepth];
   ring_pipeline(
       n, buf,
       [&](int i, Ops& o) {
@@ -405,18 +558,19 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
       },
       [&](int i, const Ops& o) {
         const int j = wave + (i / KB) * kRefWaves, kb = i % KB;
-        const ActOperand xa = lds_act(hl + (static_cast<size_t>(j) * M + row) * I + kb * kBlock, g);
+        const int hr = DENSE ? row * P + j : rtab[j * 16 + row];  // dense: token row's chunk j
+        const ActOperand xa = lds_act(hl + static_cast<size_t>(hr) * I + kb * kBlock, g);
         acc = mfma_block_bf16(o.w, o.sc, xa, acc);
         if (kb == KB - 1) {  // the slot's product is complete: add its weighted term
-          float wt;
-          token_pos(pe, pw, P, row, mask_nth(mask, j), wt);
+          const float wt = DENSE ? 1.f : wtab[j * 16 + row];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             yacc[q] += bf16_to_f32(f32_to_bf16(acc[q] * wt));
             acc[q] = 0.f;
           }
         }
-      });
+      },
+      gather);  // (ring_pipeline runs the gather even for a wave with no items: every wave meets its barriers)
 #pragma unroll
   for (int q = 0; q < 4; ++q) red[wave][q][lane] = yacc[q];
   __syncthreads();
@@ -470,9 +624,8 @@ static int launch_gate_up(bool dense, const void* x, const float* gamma, float e
 static int launch_down(bool dense, const void* h, const void* w2, const float* s2, const int32_t* idx, const float* probs,
                        const void* x_in, int64_t M, int64_t P, int64_t topk, int64_t n_local, int64_t D, int64_t I, void* y,
                        hipStream_t st) {
-  const int64_t max_hit = std::min<int64_t>(n_local, M * P);
-  const int64_t lds = max_hit * M * I * 2;
-  if (lds > 96 * 1024) { set_error("down: %lld bytes of gathered rows exceed 96 KB (M=%lld, I=%lld)", (long long)lds, (long long)M, (long long)I); return kErrUnsupported; }
+  const int64_t lds = (M * P + 1) * I * 2;  // h and one zero row
+  if (lds > 96 * 1024) { set_error("down: %lld bytes of h rows exceed 96 KB (M=%lld, P=%lld, I=%lld)", (long long)lds, (long long)M, (long long)P, (long long)I); return kErrUnsupported; }
   const void* fn = dense ? reinterpret_cast<const void*>(ref_down_kernel<true>) : reinterpret_cast<const void*>(ref_down_kernel<false>);
   if (int rc = allow_dynamic_lds(fn, 96 * 1024, "down")) return rc;
   if (dense)
@@ -501,6 +654,7 @@ static int check_routing(const char* who, int64_t M, int64_t n_routed, int64_t t
 }  // namespace tl
 
 using namespace tl;
+
 
 extern "C" int tl_moe_route(const float* scores, const float* bias, int64_t M, int64_t n_routed, int64_t topk,
                             int64_t n_groups, int64_t topk_groups, float route_scale, float* probs_out, int32_t* idx_out,
@@ -554,6 +708,7 @@ extern "C" int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, f
                                        const float* s13, int64_t M, int64_t n_chunks, int64_t D, int64_t I, void* h_bf16,
                                        void* stream) {
   const char* who = "rmsnorm_up_gate_silu";
+  if (D > 8192) { set_error("%s: D=%lld > 8192 (the norm takes two 8-element chunks per thread)", who, (long long)D); return kErrUnsupported; }
   if (n_chunks < 1 || n_chunks > kRefMaxLocal) { set_error("%s: n_chunks=%lld out of range", who, (long long)n_chunks); return kErrArg; }
   if (int rc = check_common(who, M, n_chunks, D, I)) return rc;
   if (!x_bf16 || !gamma || !w13_packed || !s13 || !h_bf16) { set_error("%s: null pointer", who); return kErrArg; }
