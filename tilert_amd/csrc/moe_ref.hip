@@ -143,8 +143,8 @@ __device__ inline float wave_sum_f32(float v) {
 // One wave per token: lane l holds routed experts l, l + 64, l + 128, l + 192.  The wave
 // is latency-bound (one wave, dependent steps), so every reduction is a register-level one:
 // groups of 32 experts (DeepSeek-V3.2's 8 groups of 256) are the two 32-lane halves of one
-// expert column, reduced with xor shuffles; each top-k round is one DPP max over
-// order-preserving keys and a ballot for the lowest expert holding it.
+// expert column, reduced with xor shuffles; each top-k round is one 64-bit DPP max over
+// (order-preserving key, expert) pairs.
 __device__ inline bool better(float v, int e, float bv, int be) { return v > bv || (v == bv && e < be); }
 
 __device__ inline uint32_t route_key(float f) {  // larger float, larger key; 0 = unavailable
@@ -152,31 +152,51 @@ __device__ inline uint32_t route_key(float f) {  // larger float, larger key; 0 
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Wave max by DPP (row shifts, then row broadcasts: lane 63 ends with the result).
-__device__ inline uint32_t route_wave_max(uint32_t x) {
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x111, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x112, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x114, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x118, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x142, 0xa, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x143, 0xc, 0xf, false)));
-  return __builtin_amdgcn_readlane(x, 63);
+
+// 64-bit wave max by DPP (row shifts, then row broadcasts: lane 63 ends with the result),
+// the same pattern on both halves, compared as one value.
+__device__ inline uint64_t route_wave_max64(uint64_t x) {
+#define TL_DPP_MAX64(ctrl, rmask)                                                                              \
+  {                                                                                                            \
+    const uint32_t lo = static_cast<uint32_t>(x), hi = static_cast<uint32_t>(x >> 32);                        \
+    const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, ctrl, rmask, 0xf, false);                        \
+    const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, ctrl, rmask, 0xf, false);                        \
+    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;                                              \
+    x = o > x ? o : x;                                                                                         \
+  }
+  TL_DPP_MAX64(0x111, 0xf)
+  TL_DPP_MAX64(0x112, 0xf)
+  TL_DPP_MAX64(0x114, 0xf)
+  TL_DPP_MAX64(0x118, 0xf)
+  TL_DPP_MAX64(0x142, 0xa)
+  TL_DPP_MAX64(0x143, 0xc)
+#undef TL_DPP_MAX64
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), 63);
+  return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
-__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ scores, const float* __restrict__ bias,
-                                                       int n, int topk, int n_groups, int topk_groups, float route_scale,
-                                                       float* __restrict__ probs, int32_t* __restrict__ idx) {
-  __shared__ float bl[kRefMaxRouted];
-  __shared__ float gscore[64];
-  __shared__ int gkeep[64];
-  const int t = blockIdx.x, lane = threadIdx.x;
+// Routing of one token by one wave (scores row `srow` [n]): on return lanes r < topk hold
+// the token's r-th expert and its normalised, scaled probability.  bl [kRefMaxRouted],
+// gscore [64] and gkeep [64] are this wave's LDS scratch (the general group path only); the
+// wave's own LDS writes are ordered before its reads (wave-scope fences), so several waves
+// of a workgroup can route tokens side by side.
+__device__ inline void route_one(const float* __restrict__ srow, const float* __restrict__ bias, int n, int topk,
+                                 int n_groups, int topk_groups, float route_scale, float* bl, float* gscore, int* gkeep,
+                                 int& out_e, float& out_p) {
+  const int lane = threadIdx.x & 63;
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
   float s[4], b[4];
   bool live[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int e = lane + 64 * i;
     live[i] = e < n;
-    const float x = scores[static_cast<size_t>(t) * n + min(e, n - 1)];
+    const float x = srow[min(e, n - 1)];
     s[i] = 1.0f / (1.0f + expf(-x));  // sigmoid
     b[i] = live[i] ? s[i] + (bias ? bias[min(e, n - 1)] : 0.f) : -INFINITY;
   }
@@ -218,7 +238,7 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (live[i]) bl[lane + 64 * i] = b[i];
-      __syncthreads();
+      wave_sync();
       if (lane < n_groups) {
         float m1 = -INFINITY, m2 = -INFINITY;
         for (int j = 0; j < gsz; ++j) {
@@ -232,56 +252,74 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
         }
         gscore[lane] = bias ? m1 + m2 : m1;
       }
-      __syncthreads();
+      wave_sync();
       if (lane < n_groups) {
         int rank = 0;
         for (int g = 0; g < n_groups; ++g) rank += better(gscore[g], g, gscore[lane], lane) ? 1 : 0;
         gkeep[lane] = rank < topk_groups;
       }
-      __syncthreads();
+      wave_sync();
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (live[i] && !gkeep[(lane + 64 * i) / gsz]) b[i] = -INFINITY;
     }
   }
-  // top-k by repeated wave arg-max (descending, lowest expert first on ties); taken and
-  // absent experts hold key 0, below every float
-  uint32_t key[4];
+  // top-k by repeated wave arg-max, descending, lowest expert first on ties: one 64-bit
+  // max per round over (key << 32 | 255 - expert) -- no branches, no ballots.  Taken and
+  // absent experts hold 0, below every candidate.
+  uint64_t ck[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) key[i] = live[i] ? route_key(b[i]) : 0u;
+  for (int i = 0; i < 4; ++i)
+    ck[i] = live[i] ? (static_cast<uint64_t>(route_key(b[i])) << 32) | static_cast<uint32_t>(255 - (lane + 64 * i)) : 0ull;
   int my_e = 0;
   float my_s = 0.f, sum = 0.f;
   for (int r = 0; r < topk; ++r) {
-    const uint32_t kmax = route_wave_max(max(max(key[0], key[1]), max(key[2], key[3])));
-    // the lowest expert with that key: the lowest column i, then the lowest lane
-    int be = 0;
-    float sv = 0.f;
-    bool found = false;
+    const uint64_t best = route_wave_max64(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
+    const int be = 255 - static_cast<int>(static_cast<uint32_t>(best));
+    const int col = be >> 6, owner = be & 63;
+    const float sc = col == 0 ? s[0] : (col == 1 ? s[1] : (col == 2 ? s[2] : s[3]));  // uniform select
+    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), owner));
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t bal = __ballot(key[i] == kmax);
-      if (!found && bal) {
-        const int owner = __builtin_ctzll(bal);
-        be = 64 * i + owner;
-        sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s[i]), owner));
-        if (lane == owner) key[i] = 0u;
-        found = true;
-      }
-    }
+    for (int i = 0; i < 4; ++i)
+      if (i == col && lane == owner) ck[i] = 0ull;
     if (lane == r) {
       my_e = be;
       my_s = sv;
     }
     sum += sv;
   }
+  out_e = my_e;
+  out_p = my_s / sum * route_scale;
+}
+
+__global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__ scores, const float* __restrict__ bias,
+                                                       int n, int topk, int n_groups, int topk_groups, float route_scale,
+                                                       float* __restrict__ probs, int32_t* __restrict__ idx) {
+  __shared__ float bl[kRefMaxRouted];
+  __shared__ float gscore[64];
+  __shared__ int gkeep[64];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  int e;
+  float p;
+  route_one(scores + static_cast<size_t>(t) * n, bias, n, topk, n_groups, topk_groups, route_scale, bl, gscore, gkeep, e, p);
   if (lane < topk) {
-    idx[t * topk + lane] = my_e;
-    probs[t * topk + lane] = my_s / sum * route_scale;
+    idx[t * topk + lane] = e;
+    probs[t * topk + lane] = p;
   }
 }
 
 // ------------------------------------------------------------------------ gate/up
 // Work item = (hit local expert, 16-row tile); a persistent grid strides over the items.
+// Routing inputs and outputs of the fused expert selection (MoE gate/up only).
+struct RouteArgs {
+  const float* scores;  // [M, n_routed]
+  const float* bias;    // [n_routed] or null
+  int n_routed, n_groups, topk_groups;
+  float route_scale;
+  float* probs_out;     // [M, topk], written by workgroup 0
+  int32_t* idx_out;     // [M, topk], written by workgroup 0
+};
+
 // x [M, D] bf16 is staged in LDS once per workgroup (DENSE: RMS-normalised there, in fp32,
 // rounded to bf16); the waves stream weight fragments kRefDepth blocks ahead and read their
 // activation operands from LDS.  The epilogue writes token r's row to every position p at
@@ -289,18 +327,45 @@ __global__ __launch_bounds__(64) void moe_route_kernel(const float* __restrict__
 template <bool DENSE>
 __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ w13,
-    const float* __restrict__ s13, const int32_t* __restrict__ idx, int M, int P, int topk, int n_local, int D, int I,
+    const float* __restrict__ s13, const RouteArgs ra, int M, int P, int topk, int n_local, int D, int I,
     uint16_t* __restrict__ h) {
   extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
-  __shared__ float red[kRefWaves - 1][2][4][64];
+  __shared__ float red[kRefWaves - 1][2][4][64];  // before the items: the waves' routing scratch
   __shared__ float ssq[16][kRefWaves];
   __shared__ int8_t ptab[64 * 16];  // [slot][token]: the position where the token uses the slot's expert, -1 none
+  __shared__ int16_t rpe[64];       // MoE: local expert of pair q (token q / P, position q % P)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int pe;
   float pw;
-  pair_lane<DENSE>(idx, nullptr, M, P, topk, n_local, pe, pw);
-  const ExpertMask mask = lanes_mask(pe);  // waits for the routing loads (MoE)
+  if (DENSE) {
+    pair_lane<true>(nullptr, nullptr, M, P, topk, n_local, pe, pw);
+  } else {
+    // The routing, fused: wave w selects the experts of tokens w, w + 8 (every workgroup
+    // does so; workgroup 0 also writes them out for the down kernel).  Position 0 is the
+    // shared expert (local 0), position 1 + r the token's r-th routed expert (local 1 + id).
+    static_assert(sizeof(red) >= sizeof(float) * kRefWaves * (kRefMaxRouted + 128), "routing scratch");
+    float* scratch = &red[0][0][0][0] + wave * (kRefMaxRouted + 128);
+    for (int t = wave; t < M; t += kRefWaves) {
+      int e;
+      float p;
+      route_one(ra.scores + static_cast<size_t>(t) * ra.n_routed, ra.bias, ra.n_routed, topk, ra.n_groups,
+                ra.topk_groups, ra.route_scale, scratch, scratch + kRefMaxRouted,
+                reinterpret_cast<int*>(scratch + kRefMaxRouted + 64), e, p);
+      if (lane < topk) {
+        rpe[t * P + 1 + lane] = static_cast<int16_t>(1 + e);
+        if (blockIdx.x == 0) {
+          ra.idx_out[t * topk + lane] = e;
+          ra.probs_out[t * topk + lane] = p;
+        }
+      }
+      if (lane == 0) rpe[t * P] = 0;
+    }
+    __syncthreads();
+    pe = lane < M * P ? rpe[lane] : -1;
+    pw = 0.f;
+  }
+  const ExpertMask mask = lanes_mask(pe);
   // x straight into LDS (no registers); waited for in the first item's ring start, after the
   // first weight fetches have been requested
   const int x16 = M * D / 8;
@@ -602,7 +667,7 @@ static int check_common(const char* who, int64_t M, int64_t P, int64_t D, int64_
 }
 
 static int launch_gate_up(bool dense, const void* x, const float* gamma, float eps, const void* w13, const float* s13,
-                          const int32_t* idx, int64_t M, int64_t P, int64_t topk, int64_t n_local, int64_t D, int64_t I,
+                          const RouteArgs& ra, int64_t M, int64_t P, int64_t topk, int64_t n_local, int64_t D, int64_t I,
                           void* h, hipStream_t st) {
   const int64_t x_bytes = M * D * 2;
   if (x_bytes > kRefLdsX) { set_error("gate/up: M * D * 2 = %lld bytes of activations exceed %d", (long long)x_bytes, kRefLdsX); return kErrUnsupported; }
@@ -612,11 +677,11 @@ static int launch_gate_up(bool dense, const void* x, const float* gamma, float e
   if (int rc = allow_dynamic_lds(fn, kRefLdsX, "gate/up")) return rc;
   if (dense)
     hipLaunchKernelGGL(ref_gate_up_kernel<true>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(x_bytes), st,
-                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, idx, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
+                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, ra, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
                        (int)I, (uint16_t*)h);
   else
     hipLaunchKernelGGL(ref_gate_up_kernel<false>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(x_bytes), st,
-                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, idx, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
+                       (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, ra, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
                        (int)I, (uint16_t*)h);
   return check_launch("gate/up");
 }
@@ -679,12 +744,9 @@ extern "C" int tl_expert_select_up_gate_silu(const void* x_bf16, const float* sc
     set_error("%s: x, weights and hidden_out must be 16-byte aligned", who);
     return kErrArg;
   }
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(moe_route_kernel, dim3(static_cast<unsigned>(M)), dim3(64), 0, st, scores, bias, (int)n_routed,
-                     (int)topk, (int)n_groups, (int)topk_groups, route_scale, probs_out, idx_out);
-  if (int rc = check_launch(who)) return rc;
-  return launch_gate_up(false, x_bf16, nullptr, 0.f, w13_packed, s13, idx_out, M, 1 + topk, topk, 1 + n_routed, D, I,
-                        h_bf16, st);
+  const RouteArgs ra{scores, bias, (int)n_routed, (int)n_groups, (int)topk_groups, route_scale, probs_out, idx_out};
+  return launch_gate_up(false, x_bf16, nullptr, 0.f, w13_packed, s13, ra, M, 1 + topk, topk, 1 + n_routed, D, I,
+                        h_bf16, (hipStream_t)stream);
 }
 
 extern "C" int tl_expert_down_allreduce(const void* h_bf16, const void* w2_packed, const float* s2, const int32_t* idx,
@@ -717,7 +779,7 @@ extern "C" int tl_rmsnorm_up_gate_silu(const void* x_bf16, const float* gamma, f
     set_error("%s: x, gamma, weights and hidden_out must be 16-byte aligned", who);
     return kErrArg;
   }
-  return launch_gate_up(true, x_bf16, gamma, eps, w13_packed, s13, nullptr, M, n_chunks, 0, n_chunks, D, I, h_bf16,
+  return launch_gate_up(true, x_bf16, gamma, eps, w13_packed, s13, RouteArgs{}, M, n_chunks, 0, n_chunks, D, I, h_bf16,
                         (hipStream_t)stream);
 }
 
