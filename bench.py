@@ -133,14 +133,14 @@ def cpu_baseline_linear(torch, q, s, xq, xs, M, N, K):
     return us, us_deq, cores
 
 
-def measured_traffic(name: str):
+def measured_traffic(name: str, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch from the committed rocprofv3 PMC summary (FETCH_SIZE +
     WRITE_SIZE, each scaled by a plain copy's reading), or None when absent."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -352,9 +352,17 @@ def bench_indexer_bf16(torch, dev):
         us = _graph_time_us(torch, lambda i: op(q, caches[i % 10], w, logits, idx, L - 4, None), CALLS, 5)
         b = L * 256 + M * H * 256 + M * H * 2 + 2 * M * L * 4 + M * k * 4
         flops = 2 * M * H * 128 * L
+        tkey = "traffic_bytes_per_launch_" + ("dsv32" if H == 64 else "glm5")
         out[name] = {"us": round(us, 2), "launches": 2, "bytes_per_call": b, "GBs": round(b / us / 1e3, 1),
                      "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                     "mfma_util_bf16": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4)}
+                     "mfma_util_bf16": round(flops / us / 1e6 / BF16_PEAK_TFLOPS, 4),
+                     "roofline": {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                  "traffic": measured_traffic("indexer_bf16_128k_M4.md", tkey),
+                                  "traffic_source": "profiles/indexer_bf16_128k_M4.md (rocprofv3 --pmc FETCH_SIZE, "
+                                                    "WRITE_SIZE; scores + top-k per call)",
+                                  "kernel": f"tl::indexer_kernel<4, {H}, {H // 4}, 2> + tl::topk_kernel<4>",
+                                  "bytes_per_call": b}}
     del caches
     return out
 
@@ -413,7 +421,14 @@ def bench_ref_layout(torch, dev):
     b = mh * (3 * I * D + 3 * (I // 128) * (D // 128) * 4) + M * D * 2 * 3 + M * 9 * I * 2 * 2
     out["moe_ref_layout_M4"] = {"us": round(us, 2), "mean_hit_experts": round(mh, 2), "bytes_per_call": round(b),
                                 "GBs": round(b / us / 1e3, 1), "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                                "routings": st}
+                                "routings": st,
+                                "roofline": {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                                             "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                             "traffic": measured_traffic("moe_ref_layout_M4.md"),
+                                             "traffic_source": "profiles/moe_ref_layout_M4.md (rocprofv3 --pmc FETCH_SIZE, "
+                                                               "WRITE_SIZE; gate/up + down per call)",
+                                             "kernel": "tl::ref_gate_up_kernel<false> + tl::ref_down_kernel<false>",
+                                             "bytes_per_call": round(b)}}
     del copies
     torch.cuda.empty_cache()
 
@@ -430,7 +445,15 @@ def bench_ref_layout(torch, dev):
     us = _graph_time_us(torch, dense_step, st, 5)
     b = 9 * 3 * I * D + M * D * 2 * 3 + M * 9 * I * 2 * 2
     out["dense_mlp_share_M4"] = {"us": round(us, 2), "bytes_per_call": b, "GBs": round(b / us / 1e3, 1),
-                                 "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+                                 "hbm_frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                 "roofline": {"bound": "hbm", "achieved": round(b / us / 1e3, 1), "peak": HBM_PEAK_GBS,
+                                              "unit": "GB/s", "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                                              "traffic": measured_traffic("moe_ref_layout_M4.md",
+                                                                          "traffic_bytes_per_launch_dense"),
+                                              "traffic_source": "profiles/moe_ref_layout_M4.md (rocprofv3 --pmc "
+                                                                "FETCH_SIZE, WRITE_SIZE; gate/up + down per call)",
+                                              "kernel": "tl::ref_gate_up_kernel<true> + tl::ref_down_kernel<true>",
+                                              "bytes_per_call": b}}
     del dense
 
     # absorbed MLA projections at the 16-head share
