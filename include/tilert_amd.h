@@ -225,8 +225,9 @@ int tl_moe_route(const float* scores, const float* bias, int64_t M, int64_t n_ro
 /* expert_select_up_gate_silu_op (deepseek_v3_2/ops/expert_sel_up_gate_silu.py:23-48; golden
  * :654-692): tl_moe_route, then for every token t and position p (0 = shared expert,
  * 1 + j = its j-th selected expert) h[t, p, :] = bf16(silu(x_t . G^T) * (x_t . U^T)).
- * x bf16 [M, D]; h bf16 [M, 1 + topk, I]; probs_out / idx_out as tl_moe_route.  Two
- * launches (routing, gate/up); only the hit experts' weights are read. */
+ * x bf16 [M, D]; h bf16 [M, 1 + topk, I]; probs_out / idx_out as tl_moe_route.  One
+ * launch (every gate/up workgroup routes the M tokens itself; workgroup 0 writes probs_out
+ * and idx_out); only the hit experts' weights are read. */
 int tl_expert_select_up_gate_silu(const void* x_bf16, const float* scores, const float* bias,
                                   const void* w13_packed, const float* s13, int64_t M, int64_t n_routed,
                                   int64_t topk, int64_t n_groups, int64_t topk_groups, float route_scale,
