@@ -45,7 +45,9 @@ constexpr int kRefMaxLocal = 64 * kRefMaskWords;
 constexpr int kRefMaxRouted = 256;          // 4 per lane in the routing wave
 constexpr int kRefLdsX = 64 * 1024;         // staged activations (x or gathered h)
 constexpr int kRefGuDepth = 2;              // gate/up weight blocks (2 fragments each) in flight per wave
-constexpr int kRefDnDepth = 6;              // down weight fragments in flight per wave
+// down weight fragments in flight per wave (measured at M = 4: the MoE's ~7 items per wave
+// are fastest at 3 (15.0 us vs 16.6 at 6), the dense share's 2-4 at 4 (8.4 vs 9.0 us))
+__host__ __device__ constexpr int ref_down_depth(bool dense) { return dense ? 4 : 3; }
 
 // Hit set over local experts, wave-uniform (scalar registers).
 struct ExpertMask {
@@ -321,7 +323,7 @@ struct RouteArgs {
 };
 
 // x [M, D] bf16 is staged in LDS once per workgroup (DENSE: RMS-normalised there, in fp32,
-// rounded to bf16); the waves stream weight fragments kRefDepth blocks ahead and read their
+// rounded to bf16); the waves stream weight fragments kRefGuDepth blocks ahead and read their
 // activation operands from LDS.  The epilogue writes token r's row to every position p at
 // which r uses the expert: h [M, P, I].
 template <bool DENSE>
@@ -612,7 +614,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
     v8i w;
     float sc;
   };
-  Ops buf[kRefDnDepth];
+  Ops buf[ref_down_depth(DENSE)];
   ring_pipeline(
       n, buf,
       [&](int i, Ops& o) {
