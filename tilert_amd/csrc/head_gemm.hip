@@ -14,10 +14,14 @@
 // output; with a residual, bf16(bf16(y) + x_in).
 //
 // Layout: W is the tile-major fragment packing of tl_moe_pack_weight applied to the
-// stacked [H * N, K] matrix; scales fp32 [H][N/128][K/128].  A workgroup stages x [M, H, K]
-// in LDS once; work item = (head, 16-row tile) over a persistent grid; its waves take the
-// K blocks round-robin (two in flight each) and are reduced through LDS in wave order.
+// stacked [H * N, K] matrix; scales fp32 [H][N/128][K/128].  Work item = (head, 16-row
+// tile) over a persistent grid; per item the workgroup loads the head's x rows [M, K] into
+// registers first, then requests its first weight fragments, and only then writes x to LDS
+// (so the x round trip overlaps the weight one, and a workgroup reads 1/H of x, not all of
+// it; with one head x is staged once, before the items); its waves take the K blocks
+// round-robin (two in flight each) and are reduced through LDS in wave order.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "moe_common.h"
@@ -26,29 +30,40 @@
 namespace tl {
 
 constexpr int kHgMaxWaves = 8;
-constexpr int kHgLdsX = 64 * 1024;
+constexpr int kHgXChunks = 4;  // 16-byte x chunks per thread and item (M * K * 2 <= 4 * 16 * 64 * waves)
 
+template <bool ONCE>
 __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ s,
     const uint16_t* __restrict__ x_in, int M, int H, int N, int K, uint16_t* __restrict__ y) {
-  extern __shared__ __align__(16) uint16_t xl[];  // [M][H][K]
+  extern __shared__ __align__(16) uint16_t xl[];  // [M][K]: the current item's head rows
   __shared__ float red[kHgMaxWaves - 1][4][64];
   const int lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int x16 = M * H * K / 8;
-  for (int c = threadIdx.x; c < x16; c += blockDim.x)
-    reinterpret_cast<u32x4*>(xl)[c] = reinterpret_cast<const u32x4*>(x)[c];
-  __syncthreads();
   const int KB = K >> 7, tiles = N >> 4, SB = (N + 127) >> 7;
   const int r = lane & 15, g = lane >> 4;
   const int row = min(r, M - 1);
   const int n = wave < KB ? (KB - wave + nw - 1) / nw : 0;  // K blocks wave + i * nw
+  const int k16 = K / 8, xk16 = M * k16;                      // 16-byte chunks of a head's rows
+  // ONCE (one head): x is staged once, before the items (measured faster there)
+  if (ONCE) {
+    for (int c = threadIdx.x; c < xk16; c += blockDim.x) reinterpret_cast<u32x4*>(xl)[c] = reinterpret_cast<const u32x4*>(x)[c];
+    __syncthreads();
+  }
   for (int item = blockIdx.x; item < H * tiles; item += gridDim.x) {
     const int h = item / tiles, rt = item - h * tiles;
     const uint8_t* wt = w + (static_cast<size_t>(h) * tiles + rt) * KB * 2048;
     const float* st = s + (static_cast<size_t>(h) * SB + ((rt * 16) >> 7)) * KB;
-    const uint16_t* xr = xl + (static_cast<size_t>(row) * H + h) * K;
+    u32x4 xs[ONCE ? 1 : kHgXChunks];  // this thread's chunks c = tid + u * blockDim of x[:, h, :]
+#pragma unroll
+    for (int u = 0; u < (ONCE ? 0 : kHgXChunks); ++u) {
+      const int c = static_cast<int>(threadIdx.x) + u * static_cast<int>(blockDim.x);
+      if (c < xk16) {
+        const int t = c / k16, kc = c - t * k16;
+        xs[u] = reinterpret_cast<const u32x4*>(x + (static_cast<size_t>(t) * H + h) * K)[kc];
+      }
+    }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     struct Ops {
       v8i w;
@@ -64,7 +79,16 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
         },
         [&](int i, const Ops& o) {
           const int kb = wave + i * nw;
-          acc = mfma_block_bf16(o.w, o.sc, lds_act(xr + kb * kBlock, g), acc);
+          acc = mfma_block_bf16(o.w, o.sc, lds_act(xl + row * K + kb * kBlock, g), acc);
+        },
+        [&] {  // behind the first weight fetches: x to LDS (the previous item's reads are done)
+          if (ONCE) return;
+#pragma unroll
+          for (int u = 0; u < (ONCE ? 0 : kHgXChunks); ++u) {
+            const int c = static_cast<int>(threadIdx.x) + u * static_cast<int>(blockDim.x);
+            if (c < xk16) reinterpret_cast<u32x4*>(xl)[c] = xs[u];
+          }
+          __syncthreads();
         });
     if (wave > 0) {
 #pragma unroll
@@ -171,20 +195,29 @@ extern "C" int tl_head_gemm_bf16(const void* x_bf16, const void* w_packed, const
     set_error("%s: N=%lld must be a positive multiple of 16 and K=%lld of 128", who, (long long)N, (long long)K);
     return kErrArg;
   }
-  const int64_t x_bytes = M * H * K * 2;
-  if (x_bytes > kHgLdsX) { set_error("%s: x of %lld bytes exceeds %d", who, (long long)x_bytes, kHgLdsX); return kErrUnsupported; }
+  const int waves = static_cast<int>(std::min<int64_t>(kHgMaxWaves, std::max<int64_t>(K / kBlock, 1)));
+  const int64_t x_bytes = M * K * 2;  // one head's rows, staged per item
+  if (x_bytes > static_cast<int64_t>(kHgXChunks) * 16 * 64 * waves) {
+    set_error("%s: one head's x rows (M * K * 2 = %lld bytes) exceed %d", who, (long long)x_bytes, kHgXChunks * 16 * 64 * waves);
+    return kErrUnsupported;
+  }
   if (!x_bf16 || !w_packed || !w_s || !y_bf16) { set_error("%s: null pointer", who); return kErrArg; }
   if ((reinterpret_cast<uintptr_t>(x_bf16) | reinterpret_cast<uintptr_t>(w_packed)) & 15 ||
       (reinterpret_cast<uintptr_t>(y_bf16) | reinterpret_cast<uintptr_t>(x_in_bf16)) & 7) {
     set_error("%s: x and weights must be 16-byte aligned, y and x_in 8-byte aligned", who);
     return kErrArg;
   }
-  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(head_gemm_kernel), kHgLdsX, who)) return rc;
   const int64_t items = H * (N / 16);
-  const int waves = static_cast<int>(std::min<int64_t>(kHgMaxWaves, std::max<int64_t>(K / kBlock, 1)));
   const int grid = static_cast<int>(std::min<int64_t>(items, 512));
-  hipLaunchKernelGGL(head_gemm_kernel, dim3(grid), dim3(waves * 64), static_cast<size_t>(x_bytes), (hipStream_t)stream,
-                     (const uint16_t*)x_bf16, (const uint8_t*)w_packed, w_s, (const uint16_t*)x_in_bf16, (int)M, (int)H,
-                     (int)N, (int)K, (uint16_t*)y_bf16);
+  auto launch = [&](auto once_tag) -> int {
+    constexpr bool ONCE = decltype(once_tag)::value;
+    if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(head_gemm_kernel<ONCE>), kHgXChunks * 16 * 64 * kHgMaxWaves, who))
+      return rc;
+    hipLaunchKernelGGL(head_gemm_kernel<ONCE>, dim3(grid), dim3(waves * 64), static_cast<size_t>(x_bytes),
+                       (hipStream_t)stream, (const uint16_t*)x_bf16, (const uint8_t*)w_packed, w_s,
+                       (const uint16_t*)x_in_bf16, (int)M, (int)H, (int)N, (int)K, (uint16_t*)y_bf16);
+    return 0;
+  };
+  if (int rc = H == 1 ? launch(std::true_type{}) : launch(std::false_type{})) return rc;
   return check_launch(who);
 }
