@@ -78,6 +78,25 @@ __device__ inline float group_scale(float amax, int scale_mode) {
   return amax * (1.0f / 448.0f);
 }
 
+// ------------------------------------------------------------- wave reductions
+// OR of a 32-bit value over the wave's 64 lanes, wave-uniform.  An inclusive OR scan on
+// DPP (row shifts by 1, 2, 4, 8 within each 16-lane row, then the row broadcasts of lanes
+// 15 and 31), read from lane 63: six VALU steps, where the same reduction through lane
+// shuffles is six dependent LDS-permute round trips.
+__device__ inline uint32_t wave_or_u32(uint32_t v) {
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x111, 0xf, 0xf, false));  // row_shr:1
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x112, 0xf, 0xf, false));  // row_shr:2
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x114, 0xf, 0xf, false));  // row_shr:4
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x118, 0xf, 0xf, false));  // row_shr:8
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+__device__ inline uint64_t wave_or_u64(uint64_t m) {
+  const uint32_t lo = wave_or_u32(static_cast<uint32_t>(m)), hi = wave_or_u32(static_cast<uint32_t>(m >> 32));
+  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+}
+
 // ---------------------------------------------------------- bf16 dequantisation
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));

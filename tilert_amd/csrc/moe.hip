@@ -38,8 +38,8 @@ constexpr int kDnHBytes = 128 * 1024;  // staged h limit of the LDS down kernel 
 constexpr int kMaxLocalExperts = 64;
 
 // Hit-expert bitmask of this shard, computed by each wave on its own (no LDS, no
-// barrier): lanes test the routed ids, one ballot per local expert... folded as a
-// 64-bit OR across the wave's lanes with cross-lane exchanges.
+// barrier): lanes test the routed ids and the 64-bit masks are OR-reduced across the
+// wave's lanes.
 __device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, int pairs, int e0, int n_local) {
   const int lane = threadIdx.x & 63;
   uint64_t m = 0;
@@ -47,17 +47,9 @@ __device__ inline uint64_t routing_mask(const int32_t* __restrict__ topk_idx, in
     const int e = topk_idx[i] - e0;
     if (e >= 0 && e < n_local) m |= 1ull << e;
   }
-  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lo |= __shfl_xor(lo, o);
-    hi |= __shfl_xor(hi, o);
-  }
-  // every lane now holds the same mask: make that visible to the compiler, so the hit
-  // count, expert ids and weight addresses derived from it live in scalar registers
-  lo = __builtin_amdgcn_readfirstlane(lo);
-  hi = __builtin_amdgcn_readfirstlane(hi);
-  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+  // wave-uniform result (read from one lane), so the hit count, expert ids and weight
+  // addresses derived from it live in scalar registers
+  return wave_or_u64(m);
 }
 
 
@@ -78,16 +70,7 @@ __device__ inline float lane_pair_weight(const float* __restrict__ topk_w, int p
 
 // Hit-expert bitmask from the lane-held pairs (pairs <= 64), wave-uniform.
 __device__ inline uint64_t lane_pairs_mask(int my_e, int n_local) {
-  const uint64_t m = (my_e >= 0 && my_e < n_local) ? (1ull << my_e) : 0ull;
-  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lo |= __shfl_xor(lo, o);
-    hi |= __shfl_xor(hi, o);
-  }
-  lo = __builtin_amdgcn_readfirstlane(lo);
-  hi = __builtin_amdgcn_readfirstlane(hi);
-  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
+  return wave_or_u64((my_e >= 0 && my_e < n_local) ? (1ull << my_e) : 0ull);
 }
 
 // Routing weight of (token r, local expert e); 0 when the token does not use it.  Pairs

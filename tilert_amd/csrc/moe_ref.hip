@@ -55,18 +55,6 @@ struct ExpertMask {
   int n;
 };
 
-__device__ inline uint64_t wave_or64(uint64_t m) {
-  uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) {
-    lo |= __shfl_xor(lo, o);
-    hi |= __shfl_xor(hi, o);
-  }
-  lo = __builtin_amdgcn_readfirstlane(lo);
-  hi = __builtin_amdgcn_readfirstlane(hi);
-  return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);
-}
-
 // The set of local experts the lanes name (e < 0: none).
 __device__ inline ExpertMask lanes_mask(int e) {
   ExpertMask m;
@@ -74,7 +62,7 @@ __device__ inline ExpertMask lanes_mask(int e) {
 #pragma unroll
   for (int k = 0; k < kRefMaskWords; ++k) {
     const uint64_t b = (e >= 64 * k && e < 64 * k + 64) ? (1ull << (e - 64 * k)) : 0ull;
-    m.w[k] = wave_or64(b);
+    m.w[k] = wave_or_u64(b);
     m.n += __builtin_popcountll(m.w[k]);
   }
   return m;
