@@ -100,22 +100,6 @@ __device__ inline void pair_lane(const int32_t* __restrict__ idx, const float* _
   w = pos == 0 ? 1.f : pw;
 }
 
-// Position of local expert e for token r (-1: the token does not use it) and its weight.
-// Every lane takes part in the shuffles.
-__device__ inline int token_pos(int pe, float pw, int P, int r, int e, float& w) {
-  int pos = -1;
-  w = 0.f;
-  for (int p = 0; p < P; ++p) {
-    const int ee = __shfl(pe, r * P + p);
-    const float ww = __shfl(pw, r * P + p);
-    if (ee == e && pos < 0) {
-      pos = p;
-      w = ww;
-    }
-  }
-  return pos;
-}
-
 // fp32 sum over the wave by DPP (row shifts, then row broadcasts; lane 63 ends with it).
 __device__ inline float wave_sum_f32(float v) {
 #define TL_DPP_ADD(ctrl, rmask) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xf, false))
@@ -166,6 +150,18 @@ __device__ inline uint64_t route_wave_max64(uint64_t x) {
   return (static_cast<uint64_t>(hi) << 32) | lo;
 }
 
+// Top-2 (m1 >= m2) of this lane's pair and the pair a DPP move brings from another lane
+// (-inf where the move has no source or the row is masked off).
+template <int CTRL, int RMASK>
+__device__ inline void top2_dpp(float& m1, float& m2) {
+  const int ninf = __builtin_bit_cast(int, -INFINITY);
+  const float o1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, m1), CTRL, RMASK, 0xf, false));
+  const float o2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, m2), CTRL, RMASK, 0xf, false));
+  const float lo = fminf(m1, o1);
+  m1 = fmaxf(m1, o1);
+  m2 = fmaxf(lo, fmaxf(m2, o2));
+}
+
 // Routing of one token by one wave (scores row `srow` [n]): on return lanes r < topk hold
 // the token's r-th expert and its normalised, scaled probability.  bl [kRefMaxRouted],
 // gscore [64] and gkeep [64] are this wave's LDS scratch (the general group path only); the
@@ -193,24 +189,25 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
   if (n_groups > 1) {  // keep the topk_groups best groups (score: top-2 sum with bias, else max)
     const int gsz = n / n_groups;
     if (gsz == 32 && n == 256) {
-      // group 2 i + (lane >= 32) is held by one 32-lane half of column i: top-2 by xor shuffles
+      // group 2 i + (lane >= 32) is held by one 32-lane half of column i: its top-2 by an
+      // inclusive DPP scan (row shifts, then row 0 into row 1 and row 2 into row 3), which
+      // leaves the half's top-2 in lanes 31 and 63
       float gs[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float m1 = b[i], m2 = -INFINITY;
-#pragma unroll
-        for (int o = 16; o >= 1; o >>= 1) {
-          const float o1 = __shfl_xor(m1, o), o2 = __shfl_xor(m2, o);
-          const float lo = fminf(m1, o1);
-          m1 = fmaxf(m1, o1);
-          m2 = fmaxf(lo, fmaxf(m2, o2));
-        }
+        top2_dpp<0x111, 0xf>(m1, m2);  // row_shr:1
+        top2_dpp<0x112, 0xf>(m1, m2);  // row_shr:2
+        top2_dpp<0x114, 0xf>(m1, m2);  // row_shr:4
+        top2_dpp<0x118, 0xf>(m1, m2);  // row_shr:8
+        top2_dpp<0x142, 0xa>(m1, m2);  // row_bcast:15
         gs[i] = bias ? m1 + m2 : m1;
       }
       // group g's score: column g / 2, half g % 2
       float gv[8];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) gv[g] = __shfl(gs[g >> 1], (g & 1) * 32);
+      for (int g = 0; g < 8; ++g)
+        gv[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs[g >> 1]), (g & 1) ? 63 : 31));
       bool keep[8];
 #pragma unroll
       for (int g = 0; g < 8; ++g) {
@@ -357,7 +354,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
   }
   const ExpertMask mask = lanes_mask(pe);
   // x straight into LDS (no registers); waited for in the first item's ring start, after the
-  // first weight fetches have been requested
+  // first weight fetches have been requested (DENSE: before them, see below)
   const int x16 = M * D / 8;
   {  // every chunk once (the copies are waited for explicitly, so their count may vary)
     const int c0 = threadIdx.x - lane;
@@ -377,6 +374,9 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
       gm[u][1] = *reinterpret_cast<const v4f*>(gamma + 8 * c + 4);
     }
   }
+  // DENSE: x and gamma are waited for before any weight fetch is issued, so the norm (in
+  // the first item's ring start) runs while the first weight fetches are in flight
+  if (DENSE) __builtin_amdgcn_s_waitcnt(0);
   if (!DENSE && wave == 0) {  // position table from the lane-held pairs
     for (int i = lane; i < 64 * 16; i += 64) ptab[i] = -1;
     if (pe >= 0) {
@@ -398,60 +398,56 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
   auto prepare = [&]() {
     if (prepared) return;
     prepared = true;
-    __builtin_amdgcn_s_waitcnt(0);
+    if (!DENSE) __builtin_amdgcn_s_waitcnt(0);  // DENSE: x and gamma were waited for before the fetches
     __syncthreads();
     if (DENSE) {
-      // every row's sum of squares at once: this thread's chunks, then one DPP wave sum per
-      // row (independent chains), then the 8 wave partials through LDS
+      // Rows one at a time in rolled loops: this runs once per workgroup between the first
+      // fetches and the first MFMA, where every wave instruction costs its issue time.
+      // Sums of squares, one DPP wave sum per row, the 8 wave partials through LDS.
       const int c16 = D / 8;
-      float acc[16];
+#pragma unroll 1
+      for (int m = 0; m < M; ++m) {
+        float a = 0.f;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+        for (int u = 0; u < kNormChunks; ++u) {
+          const int c = threadIdx.x + u * kRefWaves * 64;
+          if (c < c16) {
+            const u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
 #pragma unroll
-      for (int u = 0; u < kNormChunks; ++u) {
-        const int c = threadIdx.x + u * kRefWaves * 64;
-        if (c < c16) {
-#pragma unroll
-          for (int m = 0; m < 16; ++m) {
-            if (m < M) {
-              const u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const float lo = bf16_to_f32(v[j] & 0xffffu), hi = bf16_to_f32(v[j] >> 16);
-                acc[m] += lo * lo + hi * hi;
-              }
+            for (int j = 0; j < 4; ++j) {
+              const float lo = bf16_to_f32(v[j] & 0xffffu), hi = bf16_to_f32(v[j] >> 16);
+              a += lo * lo + hi * hi;
             }
           }
         }
-      }
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        if (m < M) {
-          const float a = wave_sum_f32(acc[m]);
-          if (lane == 0) ssq[m][wave] = a;
-        }
+        a = wave_sum_f32(a);
+        if (lane == 0) ssq[m][wave] = a;
       }
       __syncthreads();
+      // 1 / rms of row m evaluated once, in lane m; then x * (1 / rms) * gamma in fp32,
+      // rounded to bf16, in place
+      float rs_l = 0.f;
+      if (lane < M) {
+        float ss = 0.f;
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        if (m < M) {
-          float ss = 0.f;
+        for (int w = 0; w < kRefWaves; ++w) ss += ssq[lane][w];
+        rs_l = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+      }
+#pragma unroll 1
+      for (int m = 0; m < M; ++m) {
+        const float rs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rs_l), m));
 #pragma unroll
-          for (int w = 0; w < kRefWaves; ++w) ss += ssq[m][w];
-          const float rs = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+        for (int u = 0; u < kNormChunks; ++u) {
+          const int c = threadIdx.x + u * kRefWaves * 64;
+          if (c < c16) {
+            u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
 #pragma unroll
-          for (int u = 0; u < kNormChunks; ++u) {
-            const int c = threadIdx.x + u * kRefWaves * 64;
-            if (c < c16) {
-              u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {  // RNE to bf16 two at a time (v_cvt_pk_bf16_f32)
-                const float ga = gm[u][j >> 1][2 * (j & 1)], gb = gm[u][j >> 1][2 * (j & 1) + 1];
-                const v2f pr = {bf16_to_f32(v[j] & 0xffffu) * rs * ga, bf16_to_f32(v[j] >> 16) * rs * gb};
-                v[j] = bf16x2_bits(pr);
-              }
-              reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
+            for (int j = 0; j < 4; ++j) {  // RNE to bf16 two at a time (v_cvt_pk_bf16_f32)
+              const float ga = gm[u][j >> 1][2 * (j & 1)], gb = gm[u][j >> 1][2 * (j & 1) + 1];
+              const v2f pr = {bf16_to_f32(v[j] & 0xffffu) * rs * ga, bf16_to_f32(v[j] >> 16) * rs * gb};
+              v[j] = bf16x2_bits(pr);
             }
+            reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
           }
         }
       }
