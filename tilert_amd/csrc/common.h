@@ -92,6 +92,39 @@ __device__ inline uint32_t wave_or_u32(uint32_t v) {
   v |= static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x143, 0xc, 0xf, false));  // row_bcast:31
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
+// Sum / max of an fp32 value over the wave, wave-uniform: the same DPP scan (row shifts,
+// then row broadcasts; lane 63 ends with the result).
+template <bool MAX>
+__device__ inline float wave_reduce_f32(float v) {
+  auto step = [&](float o) { v = MAX ? fmaxf(v, o) : v + o; };
+  const int id = MAX ? __builtin_bit_cast(int, -INFINITY) : 0;
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x111, 0xf, 0xf, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x112, 0xf, 0xf, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x114, 0xf, 0xf, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x118, 0xf, 0xf, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x142, 0xa, 0xf, false)));
+  step(__builtin_bit_cast(float, __builtin_amdgcn_update_dpp(id, __builtin_bit_cast(int, v), 0x143, 0xc, 0xf, false)));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ inline float wave_sum_f32(float v) { return wave_reduce_f32<false>(v); }
+__device__ inline float wave_max_f32(float v) { return wave_reduce_f32<true>(v); }
+
+// Max / sum over each 16-lane row with DPP, the result in every lane of the row: swaps
+// within quads, then the half-row mirror (lane i <-> 7 - i) and the row mirror
+// (i <-> 15 - i) pair every lane with one holding the other half's partial.
+template <int CTRL, bool MAX>
+__device__ inline float dpp_combine(float x) {
+  const float y = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+  return MAX ? fmaxf(x, y) : x + y;
+}
+template <bool MAX>
+__device__ inline float row16_reduce(float v) {
+  v = dpp_combine<0xb1, MAX>(v);      // quad_perm [1, 0, 3, 2]
+  v = dpp_combine<0x4e, MAX>(v);      // quad_perm [2, 3, 0, 1]
+  v = dpp_combine<0x141, MAX>(v);     // row_half_mirror
+  return dpp_combine<0x140, MAX>(v);  // row_mirror
+}
+
 __device__ inline uint64_t wave_or_u64(uint64_t m) {
   const uint32_t lo = wave_or_u32(static_cast<uint32_t>(m)), hi = wave_or_u32(static_cast<uint32_t>(m >> 32));
   return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);

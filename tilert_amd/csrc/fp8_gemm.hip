@@ -1205,8 +1205,7 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
         }
       }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss = wave_sum_f32(ss);
     const float rs = 1.0f / sqrtf(ss / static_cast<float>(K) + eps);
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {

@@ -413,8 +413,7 @@ __global__ __launch_bounds__(256) void ki_write_kernel(const uint16_t* __restric
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  amax = row16_reduce<true>(amax);  // the group's 16 lanes
   const float sc = group_scale(amax, scale_mode);
   uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -444,12 +443,6 @@ __global__ __launch_bounds__(256) void ki_write_kernel(const uint16_t* __restric
 // cross-lane butterflies (bits 0..5).  Token t lands at row *cur_pos + t: of the bf16 key
 // cache (KI = false, the reference op's output), or quantised per token into its KI page
 // (KI = true, the format tl_ki_cache_write writes).  Rows outside the cache are dropped.
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 __device__ inline float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 template <bool KI>
@@ -468,9 +461,9 @@ __global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
   const int64_t row = static_cast<int64_t>(*cur_pos) + tok;
 
   // LayerNorm in fp32: mean, biased variance, 1 / sqrt(var + eps)
-  const float mean = wave_sum(x0 + x1) * (1.0f / 128.0f);
+  const float mean = wave_sum_f32(x0 + x1) * (1.0f / 128.0f);
   const float d0 = x0 - mean, d1 = x1 - mean;
-  const float var = wave_sum(d0 * d0 + d1 * d1) * (1.0f / 128.0f);
+  const float var = wave_sum_f32(d0 * d0 + d1 * d1) * (1.0f / 128.0f);
   const float rstd = 1.0f / sqrtf(var + eps);
   float v0 = bf16_round(d0 * rstd * w0 + b0);
   float v1 = bf16_round(d1 * rstd * w1 + b1);
@@ -501,8 +494,7 @@ __global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
     // the key's act_quant over its 128 bf16 values (as ki_write_kernel)
     const float f0 = bf16_to_f32(o0), f1 = bf16_to_f32(o1);
     float amax = fmaxf(__builtin_fabsf(f0), __builtin_fabsf(f1));
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    amax = wave_max_f32(amax);
     const float sc = group_scale(amax, scale_mode);
     uint8_t* page = pages + (row / kKiPageKeys) * kKiPageBytes;
     const int r = static_cast<int>(row % kKiPageKeys);

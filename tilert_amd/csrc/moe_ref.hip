@@ -100,19 +100,6 @@ __device__ inline void pair_lane(const int32_t* __restrict__ idx, const float* _
   w = pos == 0 ? 1.f : pw;
 }
 
-// fp32 sum over the wave by DPP (row shifts, then row broadcasts; lane 63 ends with it).
-__device__ inline float wave_sum_f32(float v) {
-#define TL_DPP_ADD(ctrl, rmask) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, rmask, 0xf, false))
-  TL_DPP_ADD(0x111, 0xf);
-  TL_DPP_ADD(0x112, 0xf);
-  TL_DPP_ADD(0x114, 0xf);
-  TL_DPP_ADD(0x118, 0xf);
-  TL_DPP_ADD(0x142, 0xa);
-  TL_DPP_ADD(0x143, 0xc);
-#undef TL_DPP_ADD
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
 // ------------------------------------------------------------------------ routing
 // One wave per token: lane l holds routed experts l, l + 64, l + 128, l + 192.  The wave
 // is latency-bound (one wave, dependent steps), so every reduction is a register-level one:

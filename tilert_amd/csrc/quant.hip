@@ -23,8 +23,7 @@ __global__ __launch_bounds__(256) void act_quant_kernel(const uint16_t* __restri
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, __builtin_fabsf(v[i]));
-#pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+  amax = row16_reduce<true>(amax);  // the group's 16 lanes
   const float sc = group_scale(amax, scale_mode);
   uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -142,8 +141,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(v[i][j], v[i][j], ss);
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = wave_sum_f32(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
@@ -171,8 +169,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_kernel(
       float amax = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(q[j]));
-#pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 16));
+      amax = row16_reduce<true>(amax);  // the group's 16 lanes
       const float sc = group_scale(amax, scale_mode);
       uint32_t lo = 0, hi = 0;
 #pragma unroll

@@ -52,22 +52,6 @@ struct MlaLds {
 
 __device__ inline v8bf_t lds_v8bf(const uint8_t* p) { return *reinterpret_cast<const v8bf_t*>(p); }
 
-// Max / sum over each 16-lane row with DPP (no LDS round trip): swaps within quads, then
-// the half-row mirror (lane i <-> 7 - i) and the row mirror (i <-> 15 - i) pair every lane
-// with one in the other half; after each step all lanes of the group hold its result.
-template <int CTRL, bool MAX>
-__device__ inline float dpp_combine(float x) {
-  const float y = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
-  return MAX ? fmaxf(x, y) : x + y;
-}
-template <bool MAX>
-__device__ inline float row16_reduce(float v) {
-  v = dpp_combine<0xb1, MAX>(v);   // quad_perm [1, 0, 3, 2]
-  v = dpp_combine<0x4e, MAX>(v);   // quad_perm [2, 3, 0, 1]
-  v = dpp_combine<0x141, MAX>(v);  // row_half_mirror
-  return dpp_combine<0x140, MAX>(v);  // row_mirror
-}
-
 template <int HT>
 __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     const uint16_t* __restrict__ q_nope, const uint16_t* __restrict__ q_pe, const uint16_t* __restrict__ kv,
