@@ -304,7 +304,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     const float* __restrict__ s13, const RouteArgs ra, int M, int P, int topk, int n_local, int D, int I,
     uint16_t* __restrict__ h) {
   extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
-  __shared__ float red[kRefWaves - 1][2][4][64];  // before the items: the waves' routing scratch
+  __shared__ v4f red[kRefWaves - 1][2][64];  // [wave][gate, up][lane]; before the items: the waves' routing scratch
   __shared__ float ssq[16][kRefWaves];
   __shared__ int8_t ptab[64 * 16];  // [slot][token]: the position where the token uses the slot's expert, -1 none
   __shared__ int16_t rpe[64];       // MoE: local expert of pair q (token q / P, position q % P)
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     // does so; workgroup 0 also writes them out for the down kernel).  Position 0 is the
     // shared expert (local 0), position 1 + r the token's r-th routed expert (local 1 + id).
     static_assert(sizeof(red) >= sizeof(float) * kRefWaves * (kRefMaxRouted + 128), "routing scratch");
-    float* scratch = &red[0][0][0][0] + wave * (kRefMaxRouted + 128);
+    float* scratch = reinterpret_cast<float*>(&red[0][0][0]) + wave * (kRefMaxRouted + 128);
     for (int t = wave; t < M; t += kRefWaves) {
       int e;
       float p;
@@ -350,20 +350,19 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(x) + cw + lane,
                                          (lds_ptr)(xl + static_cast<size_t>(cw) * 8), 16, 0, 0);
   }
-  // DENSE: this thread's gamma values for the norm (its chunks c = tid, tid + 512 of a row)
+  // DENSE: gamma [D] fp32 into LDS behind x (gl); x and gamma are waited for before any
+  // weight fetch is issued, so the row statistics (in the first item's ring start) are
+  // computed while the first weight fetches are in flight
   constexpr int kNormChunks = 2;  // D / 8 <= 1024 chunks of 8 per row
-  v4f gm[kNormChunks][2];
+  float* gl = reinterpret_cast<float*>(xl + static_cast<size_t>(M) * D);
   if (DENSE) {
-#pragma unroll
-    for (int u = 0; u < kNormChunks; ++u) {
-      const int c = min(static_cast<int>(threadIdx.x) + u * kRefWaves * 64, D / 8 - 1);
-      gm[u][0] = *reinterpret_cast<const v4f*>(gamma + 8 * c);
-      gm[u][1] = *reinterpret_cast<const v4f*>(gamma + 8 * c + 4);
-    }
+    const int g16 = D / 4, c0 = threadIdx.x - lane;
+    for (int cw = c0; cw < g16; cw += kRefWaves * 64)
+      if (cw + lane < g16)
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(gamma) + cw + lane,
+                                         (lds_ptr)(gl + static_cast<size_t>(cw) * 4), 16, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
   }
-  // DENSE: x and gamma are waited for before any weight fetch is issued, so the norm (in
-  // the first item's ring start) runs while the first weight fetches are in flight
-  if (DENSE) __builtin_amdgcn_s_waitcnt(0);
   if (!DENSE && wave == 0) {  // position table from the lane-held pairs
     for (int i = lane; i < 64 * 16; i += 64) ptab[i] = -1;
     if (pe >= 0) {
@@ -379,6 +378,8 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     }
   }
   bool prepared = false;
+  float rsv[4] = {0.f, 0.f, 0.f, 0.f};  // DENSE: 1 / rms of rows (lane >> 4) + 4 p
+  bool norm_pending = DENSE;            // DENSE: this wave's K blocks not yet normalised
   // first item's ring start: x has landed; DENSE: RMSNorm of the staged rows in place,
   // x * (1 / sqrt(mean(x^2) + eps)) * gamma in fp32, rounded to bf16 (the rows' partial sums
   // reduced together)
@@ -388,9 +389,11 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     if (!DENSE) __builtin_amdgcn_s_waitcnt(0);  // DENSE: x and gamma were waited for before the fetches
     __syncthreads();
     if (DENSE) {
-      // Rows one at a time in rolled loops: this runs once per workgroup between the first
-      // fetches and the first MFMA, where every wave instruction costs its issue time.
-      // Sums of squares, one DPP wave sum per row, the 8 wave partials through LDS.
+      // Row sums of squares, rows one at a time in rolled loops (this runs once per
+      // workgroup between the first fetches and the first MFMA, where every wave
+      // instruction costs its issue time): one DPP wave sum per row, the 8 wave partials
+      // through LDS.  Each lane then holds 1 / rms of rows (lane >> 4) + 4 p, the rows it
+      // normalises in the blocks of its wave.
       const int c16 = D / 8;
 #pragma unroll 1
       for (int m = 0; m < M; ++m) {
@@ -411,34 +414,14 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
         if (lane == 0) ssq[m][wave] = a;
       }
       __syncthreads();
-      // 1 / rms of row m evaluated once, in lane m; then x * (1 / rms) * gamma in fp32,
-      // rounded to bf16, in place
-      float rs_l = 0.f;
-      if (lane < M) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int m = min((lane >> 4) + 4 * p, M - 1);
         float ss = 0.f;
 #pragma unroll
-        for (int w = 0; w < kRefWaves; ++w) ss += ssq[lane][w];
-        rs_l = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+        for (int w = 0; w < kRefWaves; ++w) ss += ssq[m][w];
+        rsv[p] = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
       }
-#pragma unroll 1
-      for (int m = 0; m < M; ++m) {
-        const float rs = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, rs_l), m));
-#pragma unroll
-        for (int u = 0; u < kNormChunks; ++u) {
-          const int c = threadIdx.x + u * kRefWaves * 64;
-          if (c < c16) {
-            u32x4 v = reinterpret_cast<const u32x4*>(xl + m * D)[c];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {  // RNE to bf16 two at a time (v_cvt_pk_bf16_f32)
-              const float ga = gm[u][j >> 1][2 * (j & 1)], gb = gm[u][j >> 1][2 * (j & 1) + 1];
-              const v2f pr = {bf16_to_f32(v[j] & 0xffffu) * rs * ga, bf16_to_f32(v[j] >> 16) * rs * gb};
-              v[j] = bf16x2_bits(pr);
-            }
-            reinterpret_cast<u32x4*>(xl + m * D)[c] = v;
-          }
-        }
-      }
-      __syncthreads();
     }
   };
   const int KB = D >> 7, tiles = I >> 4, rows_e = 2 * I;
@@ -470,6 +453,33 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
         },
         [&](int i, const Ops& o) {
           const int kb = wave + i * kRefWaves;
+          if (DENSE && norm_pending) {
+            // RMSNorm of K block kb (this wave's own: no other wave reads it), in place:
+            // x * (1 / rms) * gamma in fp32, rounded to bf16; lane (row m, 16-byte chunk c)
+            const int c = lane & 15;
+            const v4f g0 = *reinterpret_cast<const v4f*>(gl + kb * kBlock + 8 * c);
+            const v4f g1 = *reinterpret_cast<const v4f*>(gl + kb * kBlock + 8 * c + 4);
+            const float gv[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const int m = (lane >> 4) + 4 * p;
+              if (4 * p < M && m < M) {
+                u32x4* px = reinterpret_cast<u32x4*>(xl + m * D + kb * kBlock) + c;
+                u32x4 v = *px;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {  // RNE to bf16 two at a time (v_cvt_pk_bf16_f32)
+                  const v2f pr = {bf16_to_f32(v[j] & 0xffffu) * rsv[p] * gv[2 * j],
+                                  bf16_to_f32(v[j] >> 16) * rsv[p] * gv[2 * j + 1]};
+                  v[j] = bf16x2_bits(pr);
+                }
+                *px = v;
+              }
+            }
+            // the wave's own LDS writes before its operand reads
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          }
           const uint16_t* xk = xrow + kb * kBlock;
           const int off[4] = {16 * g, 16 * g + 8, 64 + 16 * g, 64 + 16 * g + 8};
 #pragma unroll
@@ -480,22 +490,18 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
           }
         },
         prepare);
+    norm_pending = false;
     if (wave > 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        red[wave - 1][0][j][lane] = ag[j];
-        red[wave - 1][1][j][lane] = au[j];
-      }
+      red[wave - 1][0][lane] = ag;
+      red[wave - 1][1][lane] = au;
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-      for (int w = 0; w < kRefWaves - 1; ++w)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ag[j] += red[w][0][j][lane];
-          au[j] += red[w][1][j][lane];
-        }
+      for (int w = 0; w < kRefWaves - 1; ++w) {
+        ag += red[w][0][lane];
+        au += red[w][1][lane];
+      }
       const int pos = DENSE ? e : ptab[slot * 16 + min(r, M - 1)];
       if (r < M && pos >= 0) {
         uint16_t o[4];
@@ -525,7 +531,7 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ probs, const uint16_t* __restrict__ x_in, int M,
     int P, int topk, int n_local, int D, int I, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) uint16_t hl[];  // [M * P + 1][I]: h, then a zero row
-  __shared__ float red[kRefWaves][4][64];
+  __shared__ v4f red[kRefWaves][64];
   __shared__ float wtab[64 * 16];    // [slot][token]: the token's routing weight for the slot's expert (0: unused)
   __shared__ uint8_t rtab[64 * 16];  // [slot][token]: the row of hl the product reads (MoE)
   const int lane = threadIdx.x & 63;
@@ -533,11 +539,15 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
   int pe;
   float pw;
   pair_lane<DENSE>(idx, probs, M, P, topk, n_local, pe, pw);
-  const ExpertMask mask = lanes_mask(pe);
   const int KB = I >> 7;
   const int r = lane & 15, g = lane >> 4;
   const int row = min(r, M - 1);
   const int rt = blockIdx.x;
+  // the residual this lane adds at the end, requested now (after the routing loads, so
+  // waiting for those does not wait for it)
+  uint2 xres = make_uint2(0u, 0u);
+  if (x_in) xres = *reinterpret_cast<const uint2*>(x_in + static_cast<size_t>(row) * D + rt * 16 + 4 * g);
+  const ExpertMask mask = lanes_mask(pe);
   // The slot of this lane's pair's expert: the rank of pe in the hit set.  h ([M * P][I], pair
   // q = token q / P, position q % P) is copied whole into LDS, followed by one zero row; the
   // product of slot j for token t reads row rtab[j][t]: its pair's row, or the zero row when
@@ -609,21 +619,20 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_down_kernel(
         }
       },
       gather);  // (ring_pipeline runs the gather even for a wave with no items: every wave meets its barriers)
-#pragma unroll
-  for (int q = 0; q < 4; ++q) red[wave][q][lane] = yacc[q];
+  red[wave][lane] = yacc;
   __syncthreads();
   if (wave == 0 && r < M) {
     v4f s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kRefWaves; ++w)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) s[q] += red[w][q][lane];
+    for (int w = 0; w < kRefWaves; ++w) s += red[w][lane];
     uint16_t o[4];
     const size_t off = static_cast<size_t>(r) * D + rt * 16 + 4 * g;
+    const uint16_t xr[4] = {static_cast<uint16_t>(xres.x & 0xffffu), static_cast<uint16_t>(xres.x >> 16),
+                            static_cast<uint16_t>(xres.y & 0xffffu), static_cast<uint16_t>(xres.y >> 16)};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       o[q] = f32_to_bf16(s[q]);
-      if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(x_in[off + q]));
+      if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(xr[q]));
     }
     *reinterpret_cast<uint2*>(y + off) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
                                                     o[2] | (static_cast<uint32_t>(o[3]) << 16));
@@ -647,9 +656,11 @@ static int launch_gate_up(bool dense, const void* x, const float* gamma, float e
   const int64_t max_items = std::min<int64_t>(n_local, M * P) * (I / 16);
   const int grid = static_cast<int>(std::min<int64_t>(max_items, 512));
   const void* fn = dense ? reinterpret_cast<const void*>(ref_gate_up_kernel<true>) : reinterpret_cast<const void*>(ref_gate_up_kernel<false>);
-  if (int rc = allow_dynamic_lds(fn, kRefLdsX, "gate/up")) return rc;
+  // DENSE: gamma [D] fp32 (D <= 8192) lies in LDS behind x
+  const int64_t lds = x_bytes + (dense ? D * 4 : 0);
+  if (int rc = allow_dynamic_lds(fn, dense ? kRefLdsX + 8192 * 4 : kRefLdsX, "gate/up")) return rc;
   if (dense)
-    hipLaunchKernelGGL(ref_gate_up_kernel<true>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(x_bytes), st,
+    hipLaunchKernelGGL(ref_gate_up_kernel<true>, dim3(grid), dim3(kRefWaves * 64), static_cast<size_t>(lds), st,
                        (const uint16_t*)x, gamma, eps, (const uint8_t*)w13, s13, ra, (int)M, (int)P, (int)topk, (int)n_local, (int)D,
                        (int)I, (uint16_t*)h);
   else
