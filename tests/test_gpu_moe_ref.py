@@ -107,7 +107,8 @@ def test_routing_without_bias_and_ties(cuda):
 
 
 @pytest.mark.parametrize("arch,D,M", [("deepseek_v3_2", 7168, 4), ("deepseek_v3_2", 7168, 1),
-                                      ("glm_5", 6144, 2), ("deepseek_v3_2", 1024, 3)])
+                                      ("glm_5", 6144, 2), ("deepseek_v3_2", 1024, 3),
+                                      ("deepseek_v3_2", 1024, 6)])  # M > 4: every wave routes, x copied after
 def test_expert_select_up_gate_silu_and_down_vs_oracle(cuda, arch, D, M):
     I, n_routed = 256, 256
     n_groups, topk_groups, topk, scale = ROUTING[arch]

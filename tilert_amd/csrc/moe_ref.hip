@@ -319,6 +319,15 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     // does so; workgroup 0 also writes them out for the down kernel).  Position 0 is the
     // shared expert (local 0), position 1 + r the token's r-th routed expert (local 1 + id).
     static_assert(sizeof(red) >= sizeof(float) * kRefWaves * (kRefMaxRouted + 128), "routing scratch");
+    if (M <= kRefWaves / 2 && wave >= kRefWaves / 2) {
+      // waves that route no token copy x straight into LDS meanwhile (no registers)
+      const int x16 = M * D / 8, t0 = threadIdx.x - kRefWaves * 32;
+      for (int cw = t0 - lane; cw < x16; cw += kRefWaves * 32)  // cw: this wave's first chunk (uniform)
+        if (cw + lane < x16)
+          __builtin_amdgcn_global_load_lds(reinterpret_cast<const u32x4*>(x) + cw + lane,
+                                           (lds_ptr)(xl + static_cast<size_t>(cw) * 8), 16, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0);  // landed before the barrier below
+    }
     float* scratch = reinterpret_cast<float*>(&red[0][0][0]) + wave * (kRefMaxRouted + 128);
     for (int t = wave; t < M; t += kRefWaves) {
       int e;
@@ -340,10 +349,12 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     pw = 0.f;
   }
   const ExpertMask mask = lanes_mask(pe);
-  // x straight into LDS (no registers); waited for in the first item's ring start, after the
-  // first weight fetches have been requested (DENSE: before them, see below)
+  // x straight into LDS (no registers), unless the routing's idle waves did so: waited for
+  // in the first item's ring start, after the first weight fetches have been requested
+  // (DENSE: before them, see below)
+  const bool x_staged = !DENSE && M <= kRefWaves / 2;
   const int x16 = M * D / 8;
-  {  // every chunk once (the copies are waited for explicitly, so their count may vary)
+  if (!x_staged) {  // every chunk once (the copies are waited for explicitly, so their count may vary)
     const int c0 = threadIdx.x - lane;
     for (int cw = c0; cw < x16; cw += kRefWaves * 64)  // cw: this wave's first chunk (uniform)
       if (cw + lane < x16)
@@ -380,12 +391,12 @@ __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
   bool prepared = false;
   float rsv[4] = {0.f, 0.f, 0.f, 0.f};  // DENSE: 1 / rms of rows (lane >> 4) + 4 p
   bool norm_pending = DENSE;            // DENSE: this wave's K blocks not yet normalised
-  // first item's ring start: x has landed; DENSE: RMSNorm of the staged rows in place,
-  // x * (1 / sqrt(mean(x^2) + eps)) * gamma in fp32, rounded to bf16 (the rows' partial sums
-  // reduced together)
+  // first item's ring start: x has landed and is visible to every wave; DENSE: the rows'
+  // RMS statistics
   auto prepare = [&]() {
     if (prepared) return;
     prepared = true;
+    if (x_staged) return;  // landed before the routing's barrier
     if (!DENSE) __builtin_amdgcn_s_waitcnt(0);  // DENSE: x and gamma were waited for before the fetches
     __syncthreads();
     if (DENSE) {
