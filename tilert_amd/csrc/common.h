@@ -125,6 +125,19 @@ __device__ inline float row16_reduce(float v) {
   return dpp_combine<0x140, MAX>(v);  // row_mirror
 }
 
+// Max of a 32-bit unsigned value over the wave, wave-uniform (the same DPP scan).
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+#define TL_DPP_MAXU(ctrl, rmask) \
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), ctrl, rmask, 0xf, false)))
+  TL_DPP_MAXU(0x111, 0xf);
+  TL_DPP_MAXU(0x112, 0xf);
+  TL_DPP_MAXU(0x114, 0xf);
+  TL_DPP_MAXU(0x118, 0xf);
+  TL_DPP_MAXU(0x142, 0xa);
+  TL_DPP_MAXU(0x143, 0xc);
+#undef TL_DPP_MAXU
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
 __device__ inline uint64_t wave_or_u64(uint64_t m) {
   const uint32_t lo = wave_or_u32(static_cast<uint32_t>(m)), hi = wave_or_u32(static_cast<uint32_t>(m >> 32));
   return static_cast<uint64_t>(lo) | (static_cast<uint64_t>(hi) << 32);

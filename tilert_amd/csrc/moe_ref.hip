@@ -114,29 +114,6 @@ __device__ inline uint32_t route_key(float f) {  // larger float, larger key; 0 
 }
 
 
-// 64-bit wave max by DPP (row shifts, then row broadcasts: lane 63 ends with the result),
-// the same pattern on both halves, compared as one value.
-__device__ inline uint64_t route_wave_max64(uint64_t x) {
-#define TL_DPP_MAX64(ctrl, rmask)                                                                              \
-  {                                                                                                            \
-    const uint32_t lo = static_cast<uint32_t>(x), hi = static_cast<uint32_t>(x >> 32);                        \
-    const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, ctrl, rmask, 0xf, false);                        \
-    const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, ctrl, rmask, 0xf, false);                        \
-    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;                                              \
-    x = o > x ? o : x;                                                                                         \
-  }
-  TL_DPP_MAX64(0x111, 0xf)
-  TL_DPP_MAX64(0x112, 0xf)
-  TL_DPP_MAX64(0x114, 0xf)
-  TL_DPP_MAX64(0x118, 0xf)
-  TL_DPP_MAX64(0x142, 0xa)
-  TL_DPP_MAX64(0x143, 0xc)
-#undef TL_DPP_MAX64
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(x), 63);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(x >> 32), 63);
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 // Top-2 (m1 >= m2) of this lane's pair and the pair a DPP move brings from another lane
 // (-inf where the move has no source or the row is masked off).
 template <int CTRL, int RMASK>
@@ -238,24 +215,27 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
         if (live[i] && !gkeep[(lane + 64 * i) / gsz]) b[i] = -INFINITY;
     }
   }
-  // top-k by repeated wave arg-max, descending, lowest expert first on ties: one 64-bit
-  // max per round over (key << 32 | 255 - expert) -- no branches, no ballots.  Taken and
-  // absent experts hold 0, below every candidate.
-  uint64_t ck[4];
+  // top-k by repeated wave arg-max, descending, lowest expert first on ties: per round one
+  // 32-bit DPP max of the order-preserving keys, then the lowest expert holding that key from
+  // four ballots (expert lane + 64 i, so column order then lane order is expert order).
+  // Taken and absent experts hold key 0, below every candidate.
+  uint32_t ck[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    ck[i] = live[i] ? (static_cast<uint64_t>(route_key(b[i])) << 32) | static_cast<uint32_t>(255 - (lane + 64 * i)) : 0ull;
+  for (int i = 0; i < 4; ++i) ck[i] = live[i] ? route_key(b[i]) : 0u;
   int my_e = 0;
   float my_s = 0.f, sum = 0.f;
   for (int r = 0; r < topk; ++r) {
-    const uint64_t best = route_wave_max64(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
-    const int be = 255 - static_cast<int>(static_cast<uint32_t>(best));
-    const int col = be >> 6, owner = be & 63;
+    const uint32_t best = wave_max_u32(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
+    const uint64_t b0 = __ballot(ck[0] == best), b1 = __ballot(ck[1] == best), b2 = __ballot(ck[2] == best),
+                   b3 = __ballot(ck[3] == best);
+    const int col = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
+    const int owner = __builtin_ctzll(b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3)));
+    const int be = 64 * col + owner;
     const float sc = col == 0 ? s[0] : (col == 1 ? s[1] : (col == 2 ? s[2] : s[3]));  // uniform select
     const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), owner));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      if (i == col && lane == owner) ck[i] = 0ull;
+      if (i == col && lane == owner) ck[i] = 0u;
     if (lane == r) {
       my_e = be;
       my_s = sv;

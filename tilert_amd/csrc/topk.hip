@@ -211,17 +211,7 @@ __device__ inline void pick_digit(TopkShared& sh, uint32_t k_rem, uint32_t& digi
   dcount = sh.dcount;
 }
 
-// Wave max / min by DPP (row shifts, then row broadcasts: lane 63 ends with the result);
-// lanes shifted in from outside a row keep their own value (bound_ctrl off, old = x).
-__device__ inline uint32_t wave_max_u32(uint32_t x) {
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x111, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x112, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x114, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x118, 0xf, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x142, 0xa, 0xf, false)));
-  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(static_cast<int>(x), static_cast<int>(x), 0x143, 0xc, 0xf, false)));
-  return __builtin_amdgcn_readlane(x, 63);
-}
+// Wave min by the DPP max (common.h) of the complements.
 __device__ inline uint32_t wave_min_u32(uint32_t x) { return ~wave_max_u32(~x); }
 
 // Block-wide max and min of the valid keys (one LDS exchange).
