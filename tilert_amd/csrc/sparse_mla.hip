@@ -241,7 +241,9 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
 
 // One 64-thread workgroup per (head, token, quarter of the 512 dims): 2 dims per thread;
 // the 32 split rows are loaded together (unconditional, clamped; splits past n_splits
-// weigh 0).
+// weigh 0).  The split weights are computed lane-parallel (lane j: split j's lse, its
+// exponentials; max and sum by DPP) and read back per split with readlane: every lane
+// would otherwise evaluate all 64 exponentials, and this one-wave kernel is issue-bound.
 __global__ __launch_bounds__(64) void sparse_mla_combine_kernel(const float* __restrict__ out_acc,
                                                                 const float* __restrict__ lse_acc, int heads,
                                                                 int n_splits, uint16_t* __restrict__ out,
@@ -249,25 +251,19 @@ __global__ __launch_bounds__(64) void sparse_mla_combine_kernel(const float* __r
   const int h = blockIdx.x, s = blockIdx.y, quarter = blockIdx.z, tid = threadIdx.x;
   const int64_t row = static_cast<int64_t>(s) * heads + h;
   const int d0 = quarter * 128 + 2 * tid;
-  const float* la = lse_acc + row * kMlaMaxSplits;
   float2 v[kMlaMaxSplits];
 #pragma unroll
   for (int j = 0; j < kMlaMaxSplits; ++j)
     v[j] = *reinterpret_cast<const float2*>(out_acc + (row * kMlaMaxSplits + min(j, n_splits - 1)) * kMlaDim + d0);
-  float lj[kMlaMaxSplits];
-#pragma unroll
-  for (int j = 0; j < kMlaMaxSplits; ++j) lj[j] = j < n_splits ? la[min(j, n_splits - 1)] : -INFINITY;
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kMlaMaxSplits; ++j) mx = fmaxf(mx, lj[j]);
-  float sum = 0.f;
-#pragma unroll
-  for (int j = 0; j < kMlaMaxSplits; ++j) sum += lj[j] == -INFINITY ? 0.f : expf(lj[j] - mx);
+  const float lj = tid < n_splits ? lse_acc[row * kMlaMaxSplits + min(tid, kMlaMaxSplits - 1)] : -INFINITY;
+  const float mx = wave_max_f32(lj);
+  const float sum = wave_sum_f32(lj == -INFINITY ? 0.f : expf(lj - mx));
   const float L = mx == -INFINITY ? -INFINITY : mx + logf(sum);
+  const float wl = lj == -INFINITY ? 0.f : expf(lj - L);  // lane j: split j's weight
   float a0 = 0.f, a1 = 0.f;
 #pragma unroll
   for (int j = 0; j < kMlaMaxSplits; ++j) {
-    const float wj = lj[j] == -INFINITY ? 0.f : expf(lj[j] - L);
+    const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j));
     a0 += v[j].x * wj;
     a1 += v[j].y * wj;
   }
