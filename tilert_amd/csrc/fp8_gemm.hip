@@ -136,7 +136,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
     const float* __restrict__ Bs, const OutRoute out, float* __restrict__ partial,
     uint32_t* __restrict__ counters, int M, int N, int K, int kb_per_split) {
   constexpr int NA = RT * MT;  // accumulators per lane: (row tile j, token tile mt) at j * MT + mt
-  __shared__ float red[WAVES - 1][NA][4][64];
+  __shared__ v4f red[WAVES - 1][NA][64];
   const int KB = K >> 7;
   const int NT = N >> 4;
   const int ksplit = gridDim.y;
@@ -228,18 +228,14 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_gemm_kernel(
   // ---- cross-wave reduction in fixed order w0 + w1 + ... + w(WAVES-1)
   if (wave > 0) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[wave - 1][i][j][lane] = acc[i][j];
+    for (int i = 0; i < NA; ++i) red[wave - 1][i][lane] = acc[i];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < WAVES - 1; ++w)
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] += red[w][i][j][lane];
+    for (int i = 0; i < NA; ++i) acc[i] += red[w][i][lane];
 
   // lane holds output columns n0 + 16 jt + 4g + j (j = 0..3) of token mt*16 + r
   if (ksplit == 1) {
@@ -1162,7 +1158,7 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
     const float* __restrict__ Bs, uint16_t* __restrict__ q_nope, uint16_t* __restrict__ q_pe, int M, int N, int K,
     int nope, int rope) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];  // [M][K] normalised bf16 rows
-  __shared__ float red[kPqWaves - 1][4][64];
+  __shared__ v4f red[kPqWaves - 1][64];
   constexpr int KPW = kPqMaxKb / kPqWaves;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1237,15 +1233,13 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
     }
   }
   if (wave > 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) red[wave - 1][j][lane] = acc[j];
+    red[wave - 1][lane] = acc;
   }
   __syncthreads();
   if (wave != 0 || r >= M) return;
 #pragma unroll
   for (int w = 0; w < kPqWaves - 1; ++w)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] += red[w][j][lane];
+    acc += red[w][lane];
   // features f .. f+3 of token r: head f / (nope + rope), inside one 16-wide tile
   const int f = 16 * t + 4 * g, hd = nope + rope;
   const int head = f / hd, d = f % hd;

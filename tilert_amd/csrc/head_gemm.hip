@@ -37,7 +37,7 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ s,
     const uint16_t* __restrict__ x_in, int M, int H, int N, int K, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) uint16_t xl[];  // [M][K]: the current item's head rows
-  __shared__ float red[kHgMaxWaves - 1][4][64];
+  __shared__ v4f red[kHgMaxWaves - 1][64];
   const int lane = threadIdx.x & 63;
   const int nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -91,14 +91,12 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
           __syncthreads();
         });
     if (wave > 0) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[wave - 1][q][lane] = acc[q];
+      red[wave - 1][lane] = acc;
     }
     __syncthreads();
     if (wave == 0 && r < M) {
       for (int ww = 0; ww < nw - 1; ++ww)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] += red[ww][q][lane];
+        acc += red[ww][lane];
       const size_t off = (static_cast<size_t>(r) * H + h) * N + rt * 16 + 4 * g;
       uint16_t o[4];
 #pragma unroll
@@ -125,7 +123,7 @@ constexpr int kBgBlocks = 4;  // K <= 16 * 4 * 128 = 8192
 __global__ __launch_bounds__(kBgWaves * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x,
                                                                   const uint16_t* __restrict__ w, int M, int N, int K,
                                                                   uint16_t* __restrict__ y) {
-  __shared__ float red[kBgWaves - 1][4][64];
+  __shared__ v4f red[kBgWaves - 1][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
@@ -153,14 +151,12 @@ __global__ __launch_bounds__(kBgWaves * 64) void bf16_gemv_kernel(const uint16_t
     }
   }
   if (wave > 0) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) red[wave - 1][q][lane] = acc[q];
+    red[wave - 1][lane] = acc;
   }
   __syncthreads();
   if (wave == 0 && r < M) {
     for (int ww = 0; ww < kBgWaves - 1; ++ww)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q] += red[ww][q][lane];
+      acc += red[ww][lane];
     uint16_t* dst = y + static_cast<size_t>(r) * N + 16 * rt + 4 * g;
     *reinterpret_cast<uint2*>(dst) = make_uint2(f32_to_bf16(acc[0]) | (static_cast<uint32_t>(f32_to_bf16(acc[1])) << 16),
                                                 f32_to_bf16(acc[2]) | (static_cast<uint32_t>(f32_to_bf16(acc[3])) << 16));

@@ -108,7 +108,7 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
     const int32_t* __restrict__ topk_idx, int M, int topk, int e0, int n_local, int D, int I,
     uint16_t* __restrict__ h) {
   extern __shared__ __align__(16) uint16_t xl[];  // [M][D]
-  __shared__ float red[kMoeWaves - 1][2][4][64];
+  __shared__ v4f red[kMoeWaves - 1][2][64];
   // the routing and the x staging loads are in flight together (one round trip)
   const int pairs = M * topk;
   const int lane = threadIdx.x & 63;
@@ -174,21 +174,16 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_lds_kernel(
           }
         });
     if (wave > 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        red[wave - 1][0][j][lane] = ag[j];
-        red[wave - 1][1][j][lane] = au[j];
-      }
+      red[wave - 1][0][lane] = ag;
+      red[wave - 1][1][lane] = au;
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-      for (int w = 0; w < kMoeWaves - 1; ++w)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ag[j] += red[w][0][j][lane];
-          au[j] += red[w][1][j][lane];
-        }
+      for (int w = 0; w < kMoeWaves - 1; ++w) {
+        ag += red[w][0][lane];
+        au += red[w][1][lane];
+      }
       if (r < M) {
         uint16_t o[4];
 #pragma unroll
@@ -328,7 +323,7 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ w13, const float* __restrict__ s13,
     const int32_t* __restrict__ topk_idx, int M, int topk, int e0, int n_local, int D, int I,
     uint16_t* __restrict__ h) {
-  __shared__ float red[kMoeWaves - 1][2][4][64];
+  __shared__ v4f red[kMoeWaves - 1][2][64];
   const uint64_t mask = routing_mask(topk_idx, M * topk, e0, n_local);
   const int n_hit = __builtin_popcountll(mask);
   const int KB = D >> 7;
@@ -378,21 +373,16 @@ __global__ __launch_bounds__(kMoeWaves * 64, 4) void moe_gate_up_kernel(
       au = mfma_block_bf16(wu, usc, xa, au);
     }
     if (wave > 0) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        red[wave - 1][0][j][lane] = ag[j];
-        red[wave - 1][1][j][lane] = au[j];
-      }
+      red[wave - 1][0][lane] = ag;
+      red[wave - 1][1][lane] = au;
     }
     __syncthreads();
     if (wave == 0) {
 #pragma unroll
-      for (int w = 0; w < kMoeWaves - 1; ++w)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          ag[j] += red[w][0][j][lane];
-          au[j] += red[w][1][j][lane];
-        }
+      for (int w = 0; w < kMoeWaves - 1; ++w) {
+        ag += red[w][0][lane];
+        au += red[w][1][lane];
+      }
       if (tok) {
         uint16_t o[4];
 #pragma unroll
