@@ -211,12 +211,19 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     for (int ht = 0; ht < HT; ++ht) a[ht] = lds_v8bf(smem + S::P_OFF + ((ht * 16 + r) * kMlaSplit + ks * 32 + g * 8) * 2);
 #pragma unroll
     for (int d = 0; d < 8; ++d) {
-      const int dim = (wave * 8 + d) * 16 + r;
-      // keys ks*32 + 8g .. +7 of value column `dim` (rows 4 LDS banks apart: no conflicts)
-      const uint8_t* col = smem + S::KV_OFF + (ks * 32 + g * 8) * kMlaKvStride + dim * 2;
-      v8bf_t b;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) b[i] = __builtin_bit_cast(__bf16, *reinterpret_cast<const uint16_t*>(col + i * kMlaKvStride));
+      // The operand lane (column r, key group g) needs keys ks*32 + 8g .. +7 of value column
+      // 16 (8 wave + d) + r: a column of the key-major rows.  ds_read_b64_tr_b16 transposes
+      // within each 16-lane group: result element j of lane i is element i % 4 of the 4
+      // contiguous values addressed by lane 4 j + i / 4 of the group.  So lane r of group g
+      // addresses row (key) ks*32 + 8g + r / 4 (+ 4 for the upper half), values
+      // 16 (8 wave + d) + 4 (r % 4) .. +3, and receives its column's 4 (8) keys.
+      const uint8_t* src = smem + S::KV_OFF + (ks * 32 + g * 8 + (r >> 2)) * kMlaKvStride +
+                           ((wave * 8 + d) * 16 + 4 * (r & 3)) * 2;
+      typedef short v4s_t __attribute__((ext_vector_type(4)));
+      const v4s_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s_t*)(src));
+      const v4s_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s_t*)(src + 4 * kMlaKvStride));
+      const v8bf_t b = __builtin_bit_cast(v8bf_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) o[ht][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[ht], b, o[ht][d], 0, 0, 0);
     }
