@@ -445,6 +445,30 @@ __global__ __launch_bounds__(256) void ki_write_kernel(const uint16_t* __restric
 // (KI = true, the format tl_ki_cache_write writes).  Rows outside the cache are dropped.
 __device__ inline float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
+// The value of lane (lane ^ B), without an LDS round trip: DPP quad permutes for 1 and 2,
+// row shifts for 4, a row rotation for 8, and gfx950's row / half-wave swaps for 16 and 32
+// (v_permlane16_swap / v_permlane32_swap of a register with itself: the lanes a swap
+// replaces in either copy are the partners).
+template <int B>
+__device__ inline float lane_xor(float v) {
+  const int x = __builtin_bit_cast(int, v);
+  const int lane = threadIdx.x & 63;
+  if constexpr (B == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xb1, 0xf, 0xf, false));
+  if constexpr (B == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4e, 0xf, 0xf, false));
+  if constexpr (B == 4) {
+    const int up = __builtin_amdgcn_mov_dpp(x, 0x104, 0xf, 0xf, false);  // row_shl:4: lane + 4
+    const int dn = __builtin_amdgcn_mov_dpp(x, 0x114, 0xf, 0xf, false);  // row_shr:4: lane - 4
+    return __builtin_bit_cast(float, (lane & 4) ? dn : up);
+  }
+  if constexpr (B == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false));  // row_ror:8
+  if constexpr (B == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false, false);
+    return __builtin_bit_cast(float, (lane & 16) ? p[0] : p[1]);
+  }
+  const auto p = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(x), static_cast<unsigned>(x), false, false);
+  return __builtin_bit_cast(float, (lane & 32) ? p[0] : p[1]);
+}
+
 template <bool KI>
 __global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
     const uint16_t* __restrict__ x, int64_t seq, const int32_t* __restrict__ cur_pos, uint16_t* __restrict__ cache,
@@ -468,7 +492,7 @@ __global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
   float v0 = bf16_round(d0 * rstd * w0 + b0);
   float v1 = bf16_round(d1 * rstd * w1 + b1);
   // RoPE on elements 0..63 (v0 of every lane): (re, im) = (x_i, x_{i+32}) times (c, s)
-  const float p = __shfl_xor(v0, 32);
+  const float p = lane_xor<32>(v0);
   v0 = bf16_round(lane < 32 ? v0 * fc - p * fs : p * fs + v0 * fc);
   // Hadamard: bit 6 inside the lane, bits 5..0 across lanes
   {
@@ -476,13 +500,19 @@ __global__ __launch_bounds__(256) void ln_rope_rotate_kernel(
     v0 = a + b;
     v1 = a - b;
   }
-#pragma unroll
-  for (int bit = 32; bit >= 1; bit >>= 1) {
-    const float q0 = __shfl_xor(v0, bit), q1 = __shfl_xor(v1, bit);
+  auto butterfly = [&](auto bit_tag) {
+    constexpr int bit = decltype(bit_tag)::value;
+    const float q0 = lane_xor<bit>(v0), q1 = lane_xor<bit>(v1);
     const bool hi = lane & bit;
     v0 = hi ? q0 - v0 : v0 + q0;
     v1 = hi ? q1 - v1 : v1 + q1;
-  }
+  };
+  butterfly(std::integral_constant<int, 32>{});
+  butterfly(std::integral_constant<int, 16>{});
+  butterfly(std::integral_constant<int, 8>{});
+  butterfly(std::integral_constant<int, 4>{});
+  butterfly(std::integral_constant<int, 2>{});
+  butterfly(std::integral_constant<int, 1>{});
   constexpr float kScale = 0.08838834764831845f;  // fp32(128^-1/2)
   const uint16_t o0 = f32_to_bf16(v0 * kScale), o1 = f32_to_bf16(v1 * kScale);
   if (row < 0 || row >= cache_rows) return;  // wave-uniform: outside the cache
