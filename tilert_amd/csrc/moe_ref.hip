@@ -27,8 +27,9 @@
 // bf16 weights (expert_sel_up_gate_silu.py:545-552, expert_down_allreduce.py:389-393).
 //
 // Each token's (position -> local expert, weight) pairs are held one per lane (pair p =
-// token p / P, position p % P; M * P <= 64), so hit sets, output positions and routing
-// weights are lane shuffles, with no host synchronisation and no dependent loads.
+// token p / P, position p % P; M * P <= 64), so hit sets are wave reductions and output
+// positions and routing weights small LDS tables, with no host synchronisation and no
+// dependent loads.
 #include <math.h>
 
 #include <algorithm>
@@ -275,9 +276,10 @@ struct RouteArgs {
 };
 
 // x [M, D] bf16 is staged in LDS once per workgroup (DENSE: RMS-normalised there, in fp32,
-// rounded to bf16); the waves stream weight fragments kRefGuDepth blocks ahead and read their
-// activation operands from LDS.  The epilogue writes token r's row to every position p at
-// which r uses the expert: h [M, P, I].
+// rounded to bf16, each wave normalising its own K blocks in its first pass); the waves
+// stream weight fragments kRefGuDepth blocks ahead and read their activation operands from
+// LDS.  The epilogue writes token r's row to every position p at which r uses the expert:
+// h [M, P, I].
 template <bool DENSE>
 __global__ __launch_bounds__(kRefWaves * 64, 2) void ref_gate_up_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ gamma, float eps, const uint8_t* __restrict__ w13,
