@@ -214,8 +214,8 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
     int n_local, int D, int I, int sb, uint16_t* __restrict__ y) {
   extern __shared__ __align__(16) uint8_t smem[];
   uint16_t* hl = reinterpret_cast<uint16_t*>(smem);  // [sb][M][I] during the stream
-  float(*red)[kDnSlots][4][64] = reinterpret_cast<float(*)[kDnSlots][4][64]>(smem);  // after it
-  float(*term)[kDnSlots][4][64] = reinterpret_cast<float(*)[kDnSlots][4][64]>(smem + TPW * kDownRedBytes);
+  v4f(*red)[kDnSlots][64] = reinterpret_cast<v4f(*)[kDnSlots][64]>(smem);  // after it
+  v4f(*term)[kDnSlots][64] = reinterpret_cast<v4f(*)[kDnSlots][64]>(smem + TPW * kDownRedBytes);
   const int pairs = M * topk;
   const int my_e = lane_pair_expert(topk_idx, pairs, e0);
   const float my_w = lane_pair_weight(topk_w, pairs);
@@ -287,23 +287,20 @@ __global__ __launch_bounds__(kDownWaves * 64 * TPW, 4) void moe_down_lds_kernel(
     __syncthreads();  // every wave is done with hl before it becomes the partials
 #pragma unroll
     for (int j = 0; j < kDnSlots; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[wave][j][q][lane] = acc[j][q];
+      if (j < ns) red[wave][j][lane] = acc[j];  // (slots past the batch hold nothing)
     __syncthreads();
     if (wl < ns) {
       v4f t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < kDownWaves; ++w)
+      for (int w = 0; w < kDownWaves; ++w) t += red[tt * kDownWaves + w][wl][lane];
+      v4f tw;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) t[q] += red[tt * kDownWaves + w][wl][q][lane];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) term[tt][wl][q][lane] = bf16_to_f32(f32_to_bf16(t[q] * wj));
+      for (int q = 0; q < 4; ++q) tw[q] = bf16_to_f32(f32_to_bf16(t[q] * wj));
+      term[tt][wl][lane] = tw;
     }
     __syncthreads();
     if (wl == 0) {
-      for (int j = 0; j < ns; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) yacc[q] += term[tt][j][q][lane];
+      for (int j = 0; j < ns; ++j) yacc += term[tt][j][lane];
     }
     __syncthreads();
   }
