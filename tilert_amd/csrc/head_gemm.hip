@@ -64,6 +64,10 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
         xs[u] = reinterpret_cast<const u32x4*>(x + (static_cast<size_t>(t) * H + h) * K)[kc];
       }
     }
+    // the residual this lane adds, requested now rather than after the reduction
+    const size_t off = (static_cast<size_t>(row) * H + h) * N + rt * 16 + 4 * g;
+    uint2 xres = make_uint2(0u, 0u);
+    if (x_in) xres = *reinterpret_cast<const uint2*>(x_in + off);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
     struct Ops {
       v8i w;
@@ -97,12 +101,13 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
     if (wave == 0 && r < M) {
       for (int ww = 0; ww < nw - 1; ++ww)
         acc += red[ww][lane];
-      const size_t off = (static_cast<size_t>(r) * H + h) * N + rt * 16 + 4 * g;
+      const uint16_t xr[4] = {static_cast<uint16_t>(xres.x & 0xffffu), static_cast<uint16_t>(xres.x >> 16),
+                              static_cast<uint16_t>(xres.y & 0xffffu), static_cast<uint16_t>(xres.y >> 16)};
       uint16_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         o[q] = f32_to_bf16(acc[q]);
-        if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(x_in[off + q]));
+        if (x_in) o[q] = f32_to_bf16(bf16_to_f32(o[q]) + bf16_to_f32(xr[q]));
       }
       *reinterpret_cast<uint2*>(y + off) = make_uint2(o[0] | (static_cast<uint32_t>(o[1]) << 16),
                                                       o[2] | (static_cast<uint32_t>(o[3]) << 16));
