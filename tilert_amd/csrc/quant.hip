@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void weight_quant_kernel(const T* __restrict__
   red[threadIdx.x] = amax;
   __syncthreads();
   for (int o = 128; o > 0; o >>= 1) {
-    if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
+    if (static_cast<int>(threadIdx.x) < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
     __syncthreads();
   }
   amax = red[0];

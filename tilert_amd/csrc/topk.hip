@@ -57,8 +57,6 @@ constexpr int kMaxCols = 262144;
 constexpr int kMaxChunks = 256;                       // per row
 constexpr int kSamplePerThread = 4;
 constexpr int kSample = kTkThreads * kSamplePerThread;  // 4096
-constexpr int kCandPerThread = 8;                     // stage-2 register batch per thread
-constexpr int kCandBatch = kTkThreads * kCandPerThread;
 constexpr int kMaxRowsPerLaunch = 1024;               // arrival-counter slots
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
