@@ -173,14 +173,17 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
 #pragma unroll
       for (int g = 0; g < 8; ++g)
         gv[g] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs[g >> 1]), (g & 1) ? 63 : 31));
+      // lane g < 8 ranks group g against the other seven; the kept groups are a ballot
+      float mine = gv[0];
+#pragma unroll
+      for (int g = 1; g < 8; ++g) mine = lane == g ? gv[g] : mine;
+      int rank = 0;
+#pragma unroll
+      for (int h = 0; h < 8; ++h) rank += better(gv[h], h, mine, lane) ? 1 : 0;
+      const uint32_t keep_bits = static_cast<uint32_t>(__ballot(lane < 8 && rank < topk_groups));
       bool keep[8];
 #pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        int rank = 0;
-#pragma unroll
-        for (int h = 0; h < 8; ++h) rank += better(gv[h], h, gv[g], g) ? 1 : 0;
-        keep[g] = rank < topk_groups;
-      }
+      for (int g = 0; g < 8; ++g) keep[g] = (keep_bits >> g) & 1u;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool k0 = keep[2 * i], k1 = keep[2 * i + 1];
@@ -225,7 +228,7 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
   for (int i = 0; i < 4; ++i) ck[i] = live[i] ? route_key(b[i]) : 0u;
   int my_e = 0;
   float my_s = 0.f, sum = 0.f;
-  for (int r = 0; r < topk; ++r) {
+  auto round = [&](int r) __attribute__((always_inline)) {
     const uint32_t best = wave_max_u32(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
     const uint64_t b0 = __ballot(ck[0] == best), b1 = __ballot(ck[1] == best), b2 = __ballot(ck[2] == best),
                    b3 = __ballot(ck[3] == best);
@@ -242,6 +245,12 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
       my_s = sv;
     }
     sum += sv;
+  };
+  if (topk == 8) {  // both models' k: the rounds unrolled
+#pragma unroll
+    for (int r = 0; r < 8; ++r) round(r);
+  } else {
+    for (int r = 0; r < topk; ++r) round(r);
   }
   out_e = my_e;
   out_p = my_s / sum * route_scale;
