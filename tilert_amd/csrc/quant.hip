@@ -104,84 +104,96 @@ __global__ __launch_bounds__(256) void weight_dequant_kernel(const uint8_t* __re
 
 // RMSNorm (tilert/models/common.py:92-133, no residual): y = bf16(gamma * x * rsqrt(mean(x^2)
 // + eps)) in fp32, then -- when y8/ys are given -- act_quant of those bf16 values per
-// 1x128 group (rmsnorm_quant_op, ops/rmsnorm_quant.py:19-63).  One 1024-thread workgroup
-// per row; thread t takes the 8-element chunks t and t+1024, so 16 consecutive threads
-// hold one 128-element group.  Every load (x and gamma) is issued up front: the row costs
-// one memory round trip.  rsqrt is 1 / sqrt with IEEE sqrt and division, as torch's.
-constexpr int kNormThreads = 1024;
-constexpr int kNormMaxChunks = 2;  // dim <= 2 * 1024 * 8 = 16384
+// 1x128 group (rmsnorm_quant_op, ops/rmsnorm_quant.py:19-63).  rsqrt is 1 / sqrt with IEEE
+// sqrt and division, as torch's.
+// A row's sum of squares is taken over a fixed tree of kNormVirt virtual threads: virtual
+// thread v adds the squares of chunks (8 elements) v, v + kNormVirt, ... in order, each
+// 64 virtual threads are one DPP wave reduction, and the kNormVirt / 64 wave partials are
+// added in order -- the same float result whatever the launch shape.  The row is then cut
+// into slices of kNormSlice chunks, one 256-thread workgroup each (thread = one chunk, 16
+// threads = one 128-element group): every workgroup of a row recomputes the row's sum
+// (the row is 8-32 KB, read from L2 after the first) and normalises and quantises only
+// its slice.  One 1024-thread workgroup per row left a decode step's 4 rows on 4 CUs,
+// issue-bound on the quantisation (5.2 us at 4 x 7168).
+constexpr int kNormThreads = 256;
+constexpr int kNormVirt = 1024;
+constexpr int kNormPerThread = kNormVirt / kNormThreads;  // virtual threads per thread
+constexpr int kNormMaxChunks = 2;                           // chunks per virtual thread
+constexpr int kNormSlice = kNormThreads;                    // chunks per workgroup
+constexpr int kNormMaxDim = kNormMaxChunks * kNormVirt * 8;  // 16384
 
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_quant_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ gamma, float eps, int dim,
     uint16_t* __restrict__ y, uint8_t* __restrict__ y8, float* __restrict__ ys, int scale_mode) {
-  __shared__ float part[kNormThreads / 64];
-  const int row = blockIdx.x;
+  __shared__ float part[kNormVirt / 64];
+  const int row = blockIdx.x, tid = threadIdx.x;
   const int nch = dim / 8;
+  const int c = blockIdx.y * kNormSlice + tid;  // this thread's chunk
+  const bool live = c < nch;
   const uint4* xr = reinterpret_cast<const uint4*>(x + static_cast<int64_t>(row) * dim);
-  uint4 raw[kNormMaxChunks];
-  float4 g0[kNormMaxChunks], g1[kNormMaxChunks];
+  // every load up front (clamped, unconditional): the row for the sum, this chunk, gamma
+  uint4 raw[kNormPerThread][kNormMaxChunks];
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {  // clamped, unconditional loads
-    const int c = min(static_cast<int>(threadIdx.x) + i * kNormThreads, nch - 1);
-    raw[i] = xr[c];
-    g0[i] = reinterpret_cast<const float4*>(gamma)[2 * c];
-    g1[i] = reinterpret_cast<const float4*>(gamma)[2 * c + 1];
-  }
-  float v[kNormMaxChunks][8];
-  float ss = 0.f;
+  for (int u = 0; u < kNormPerThread; ++u)
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    const bool live = static_cast<int>(threadIdx.x) + i * kNormThreads < nch;
-    const uint32_t w4[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+    for (int i = 0; i < kNormMaxChunks; ++i) raw[u][i] = xr[min(tid + u * kNormThreads + i * kNormVirt, nch - 1)];
+  const int cc = min(c, nch - 1);
+  const uint4 mine = xr[cc];
+  const float4 g0 = reinterpret_cast<const float4*>(gamma)[2 * cc];
+  const float4 g1 = reinterpret_cast<const float4*>(gamma)[2 * cc + 1];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      v[i][2 * j] = live ? bf16_to_f32(w4[j] & 0xffff) : 0.f;
-      v[i][2 * j + 1] = live ? bf16_to_f32(w4[j] >> 16) : 0.f;
+  for (int u = 0; u < kNormPerThread; ++u) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormMaxChunks; ++i) {
+      const bool in = tid + u * kNormThreads + i * kNormVirt < nch;
+      const uint32_t w4[4] = {raw[u][i].x, raw[u][i].y, raw[u][i].z, raw[u][i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = in ? bf16_to_f32(w4[j] & 0xffff) : 0.f;
+        const float hi = in ? bf16_to_f32(w4[j] >> 16) : 0.f;
+        ss = __builtin_fmaf(lo, lo, ss);
+        ss = __builtin_fmaf(hi, hi, ss);
+      }
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(v[i][j], v[i][j], ss);
+    ss = wave_sum_f32(ss);
+    if ((tid & 63) == 0) part[(tid >> 6) + u * (kNormThreads / 64)] = ss;
   }
-  ss = wave_sum_f32(ss);
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   float tot = 0.f;
 #pragma unroll
-  for (int w = 0; w < kNormThreads / 64; ++w) tot += part[w];
+  for (int w = 0; w < kNormVirt / 64; ++w) tot += part[w];
   const float r = 1.0f / __builtin_sqrtf(tot / static_cast<float>(dim) + eps);
+  const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+  const uint32_t w4[4] = {mine.x, mine.y, mine.z, mine.w};
+  uint16_t b[8];
+  float q[8];
 #pragma unroll
-  for (int i = 0; i < kNormMaxChunks; ++i) {
-    if (i * kNormThreads >= nch) break;  // workgroup-uniform
-    const int c = static_cast<int>(threadIdx.x) + i * kNormThreads;
-    const bool live = c < nch;
-    const float gv[8] = {g0[i].x, g0[i].y, g0[i].z, g0[i].w, g1[i].x, g1[i].y, g1[i].z, g1[i].w};
-    uint16_t b[8];
-    float q[8];
+  for (int j = 0; j < 4; ++j) {
+    b[2 * j] = f32_to_bf16(gv[2 * j] * (bf16_to_f32(w4[j] & 0xffff) * r));
+    b[2 * j + 1] = f32_to_bf16(gv[2 * j + 1] * (bf16_to_f32(w4[j] >> 16) * r));
+  }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      b[j] = f32_to_bf16(gv[j] * (v[i][j] * r));
-      q[j] = bf16_to_f32(b[j]);
-    }
-    if (live)
-      reinterpret_cast<uint4*>(y + static_cast<int64_t>(row) * dim)[c] =
-          make_uint4(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16),
-                     b[4] | (static_cast<uint32_t>(b[5]) << 16), b[6] | (static_cast<uint32_t>(b[7]) << 16));
-    if (y8) {  // kernel-uniform
-      float amax = 0.f;
+  for (int j = 0; j < 8; ++j) q[j] = bf16_to_f32(b[j]);
+  if (live)
+    reinterpret_cast<uint4*>(y + static_cast<int64_t>(row) * dim)[c] =
+        make_uint4(b[0] | (static_cast<uint32_t>(b[1]) << 16), b[2] | (static_cast<uint32_t>(b[3]) << 16),
+                   b[4] | (static_cast<uint32_t>(b[5]) << 16), b[6] | (static_cast<uint32_t>(b[7]) << 16));
+  if (!y8) return;  // kernel-uniform
+  float amax = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(q[j]));
-      amax = row16_reduce<true>(amax);  // the group's 16 lanes
-      const float sc = group_scale(amax, scale_mode);
-      uint32_t lo = 0, hi = 0;
+  for (int j = 0; j < 8; ++j) amax = fmaxf(amax, __builtin_fabsf(q[j]));
+  amax = row16_reduce<true>(amax);  // the group's 16 lanes
+  const float sc = group_scale(amax, scale_mode);
+  uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        lo |= f32_to_e4m3(fminf(fmaxf(q[j] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
-        hi |= f32_to_e4m3(fminf(fmaxf(q[j + 4] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
-      }
-      if (live) {
-        reinterpret_cast<uint2*>(y8 + static_cast<int64_t>(row) * dim)[c] = make_uint2(lo, hi);
-        if ((c & 15) == 0) ys[static_cast<int64_t>(row) * (dim / kBlock) + (c >> 4)] = sc;
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    lo |= f32_to_e4m3(fminf(fmaxf(q[j] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
+    hi |= f32_to_e4m3(fminf(fmaxf(q[j + 4] / sc, -kE4m3Max), kE4m3Max)) << (8 * j);
+  }
+  if (live) {
+    reinterpret_cast<uint2*>(y8 + static_cast<int64_t>(row) * dim)[c] = make_uint2(lo, hi);
+    if ((c & 15) == 0) ys[static_cast<int64_t>(row) * (dim / kBlock) + (c >> 4)] = sc;
   }
 }
 
@@ -191,9 +203,9 @@ using namespace tl;
 
 extern "C" int tl_rmsnorm_quant(const void* x_bf16, const float* gamma, float eps, int64_t rows, int64_t dim,
                                 void* y_bf16, void* y_fp8, float* y_scale, int scale_mode, void* stream) {
-  if (rows < 0 || dim <= 0 || dim % kBlock || dim > kNormMaxChunks * kNormThreads * 8) {
+  if (rows < 0 || dim <= 0 || dim % kBlock || dim > kNormMaxDim) {
     set_error("rmsnorm_quant: dim=%lld must be a positive multiple of 128, at most %d", (long long)dim,
-              kNormMaxChunks * kNormThreads * 8);
+              kNormMaxDim);
     return kErrArg;
   }
   if (scale_mode < 0 || scale_mode > 2) { set_error("rmsnorm_quant: bad scale_mode %d", scale_mode); return kErrArg; }
@@ -207,7 +219,9 @@ extern "C" int tl_rmsnorm_quant(const void* x_bf16, const float* gamma, float ep
     return kErrArg;
   }
   if (rows == 0) return kOk;
-  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNormThreads), 0,
+  if (rows > 0x7fffffff) { set_error("rmsnorm_quant: too many rows (%lld)", (long long)rows); return kErrArg; }
+  const unsigned slices = static_cast<unsigned>(cdiv(dim / 8, kNormSlice));
+  hipLaunchKernelGGL(rmsnorm_quant_kernel, dim3(static_cast<unsigned>(rows), slices), dim3(kNormThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x_bf16, gamma, eps, (int)dim, (uint16_t*)y_bf16,
                      (uint8_t*)y_fp8, y_scale, scale_mode);
   return check_launch("rmsnorm_quant");

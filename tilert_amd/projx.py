@@ -113,7 +113,7 @@ def rmsnorm_projx_wqkva(x: torch.Tensor, gamma: torch.Tensor, wqkva: PackedWqkva
     (RMSNorm + act_quant, one launch) into scratch tensors, then ``projx_wqkva``.  x bf16
     [batch, seq, dim]; gamma [dim]; outputs as for ``projx_wqkva``; ``x_rmsnorm_out`` (bf16,
     x's shape), when given, receives the normalised rows.  A single launch that recomputes
-    the norm in every GEMV workgroup measured slower on MI355X (20.8 vs 11.0 us at M = 4,
+    the norm in every GEMV workgroup measured slower on MI355X (15.4-20.8 vs 11.0 us at M = 4,
     7168 -> 2112): each of its 132 workgroups quantises all M x 7168 values."""
     from .rmsnorm import rmsnorm_quant
     if x.dim() != 3 or x.dtype != torch.bfloat16:
