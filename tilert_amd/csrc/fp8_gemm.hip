@@ -1164,7 +1164,29 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int KB = K >> 7, NT = N >> 4, t = blockIdx.x;
-  // this wave's weight fragments and scales first (unconditional; blocks past K weigh 0)
+  // gamma and this wave's first row first (L2-resident: they land while the weight
+  // fragments are in flight, so the norm below waits for them alone -- memory operations
+  // complete in order); lane l holds elements 8 l + 512 i .. +7 (16-byte loads; chunks
+  // past K reload chunk 0 and are not used)
+  constexpr int CPL = kPqMaxKb * kBlock / 512;  // chunks per lane
+  typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+  const int nch = K >> 9;
+  auto chunk0 = [&](int i) { return i < nch ? 512 * i + 8 * lane : 8 * lane; };
+  auto load_row = [&](int m, u32x4q (&xv)[CPL]) {
+    const uint16_t* row = q + static_cast<size_t>(m) * K;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) xv[i] = *reinterpret_cast<const u32x4q*>(row + chunk0(i));
+  };
+  v4f g0[CPL], g1[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    g0[i] = *reinterpret_cast<const v4f*>(gamma + chunk0(i));
+    g1[i] = *reinterpret_cast<const v4f*>(gamma + chunk0(i) + 4);
+  }
+  u32x4q xv[CPL];
+  load_row(min(wave, M - 1), xv);
+  __builtin_amdgcn_sched_barrier(0);  // issued ahead of the weight loads
+  // this wave's weight fragments and scales (unconditional; blocks past K weigh 0)
   v8i wf[KPW];
   float ws[KPW];
 #pragma unroll
@@ -1173,23 +1195,10 @@ __global__ __launch_bounds__(kPqWaves * 64) void rmsnorm_projq_kernel(
     wf[i] = load_packed_fragment(B + packed_fragment(t, kb, NT), lane);
     ws[i] = wave + i * kPqWaves < KB ? Bs[static_cast<size_t>((16 * t) >> 7) * KB + kb] : 0.f;
   }
-  // normalised rows: x * rsqrt(mean(x^2) + eps) * gamma in fp32, rounded to bf16.  Lane l
-  // holds elements 8 l + 512 i .. +7 (16-byte loads, all issued together; chunks past K
-  // reload chunk 0 and are not used)
-  constexpr int CPL = kPqMaxKb * kBlock / 512;  // chunks per lane
-  typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
-  const int nch = K >> 9;
+  __builtin_amdgcn_sched_barrier(0);
+  // normalised rows: x * rsqrt(mean(x^2) + eps) * gamma in fp32, rounded to bf16
   for (int m = wave; m < M; m += kPqWaves) {
-    const uint16_t* row = q + static_cast<size_t>(m) * K;
-    u32x4q xv[CPL];
-    v4f g0[CPL], g1[CPL];
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      const int k0 = i < nch ? 512 * i + 8 * lane : 8 * lane;
-      xv[i] = *reinterpret_cast<const u32x4q*>(row + k0);
-      g0[i] = *reinterpret_cast<const v4f*>(gamma + k0);
-      g1[i] = *reinterpret_cast<const v4f*>(gamma + k0 + 4);
-    }
+    if (m != wave) load_row(m, xv);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
