@@ -86,16 +86,7 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
                    : reinterpret_cast<const u32x4s*>(q_pe + (static_cast<int64_t>(s) * heads + h) * kMlaPe)[k - 64];
   }
   if (tid < kMlaSplit) idx_l[tid] = t_idx;
-#pragma unroll
-  for (int u = 0; u < QPT; ++u) {
-    const int c = tid + u * kMlaThreads;
-    if (c < QCH) {
-      const int h = c / 72, k = c % 72;
-      const u32x4s z = {0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4s*>(smem + S::Q_OFF + h * (kMlaDim + kMlaPe) * 2 + k * 16) = h < heads ? qv[u] : z;
-    }
-  }
-  __syncthreads();
+  __syncthreads();  // the positions (the queries go to LDS once the gather is in flight)
   // gather: kv row of position idx_l[row] into LDS row `row` (64 chunks of 16 B), pe row
   // (8 chunks); a masked row is loaded from row 0 (unconditional loads) and stored as
   // zeros, so whatever row 0 holds cannot reach the products
@@ -114,6 +105,14 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
       w[u] = reinterpret_cast<const u32x4s*>(pe + static_cast<int64_t>(t) * kMlaPe)[ch];
     }
     const u32x4s zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
+      const int c = tid + u * kMlaThreads;
+      if (c < QCH) {
+        const int h = c / 72, k = c % 72;
+        *reinterpret_cast<u32x4s*>(smem + S::Q_OFF + h * (kMlaDim + kMlaPe) * 2 + k * 16) = h < heads ? qv[u] : zero;
+      }
+    }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
       const int c = tid + u * kMlaThreads, row = c >> 6, ch = c & 63;
