@@ -257,11 +257,15 @@ __global__ __launch_bounds__(64) void sparse_mla_combine_kernel(const float* __r
   const int h = blockIdx.x, s = blockIdx.y, quarter = blockIdx.z, tid = threadIdx.x;
   const int64_t row = static_cast<int64_t>(s) * heads + h;
   const int d0 = quarter * 128 + 2 * tid;
+  // the split lse first: memory operations complete in order, so the weights below are
+  // computed while the split rows are still arriving
+  const float lj = tid < n_splits ? lse_acc[row * kMlaMaxSplits + min(tid, kMlaMaxSplits - 1)] : -INFINITY;
+  __builtin_amdgcn_sched_barrier(0);
   float2 v[kMlaMaxSplits];
 #pragma unroll
   for (int j = 0; j < kMlaMaxSplits; ++j)
     v[j] = *reinterpret_cast<const float2*>(out_acc + (row * kMlaMaxSplits + min(j, n_splits - 1)) * kMlaDim + d0);
-  const float lj = tid < n_splits ? lse_acc[row * kMlaMaxSplits + min(tid, kMlaMaxSplits - 1)] : -INFINITY;
+  __builtin_amdgcn_sched_barrier(0);
   const float mx = wave_max_f32(lj);
   const float sum = wave_sum_f32(lj == -INFINITY ? 0.f : expf(lj - mx));
   const float L = mx == -INFINITY ? -INFINITY : mx + logf(sum);
