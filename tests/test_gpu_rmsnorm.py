@@ -25,6 +25,8 @@ def _bf16_ulps(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     (7, 6144, "div"),    # GLM-5 hidden size
     (1, 128, "ue8m0"),
     (33, 16384, None),   # the largest supported row
+    (2, 2176, None),     # 272 chunks: a second row slice with 16 live chunks
+    (3, 10240, "ue8m0"),  # 1280 chunks: the first 256 virtual threads sum two chunks
 ])
 def test_rmsnorm_quant_vs_oracle(cuda, rows, dim, scale_fmt):
     g = synth.gen(rows * 1000 + dim)
