@@ -45,8 +45,9 @@ struct MlaLds {
   static constexpr int PE_OFF = KV_OFF + kMlaSplit * kMlaKvStride;
   static constexpr int Q_OFF = PE_OFF + kMlaSplit * kMlaPe * 2;          // [HT*16][576] bf16
   static constexpr int P_OFF = Q_OFF + HT * 16 * (kMlaDim + kMlaPe) * 2;  // [HT*16][64] bf16
-  static constexpr int RED_OFF = P_OFF + HT * 16 * kMlaSplit * 2;         // [4 waves][HT*16] f32
-  static constexpr int IDX_OFF = RED_OFF + 4 * HT * 16 * 4;               // [64] i32
+  static constexpr int RED_OFF = P_OFF + HT * 16 * kMlaSplit * 2;         // [4 waves][HT*16] f32 maxima
+  static constexpr int SUM_OFF = RED_OFF + 4 * HT * 16 * 4;               // [4 waves][HT*16] f32 sums
+  static constexpr int IDX_OFF = SUM_OFF + 4 * HT * 16 * 4;               // [64] i32
   static constexpr int BYTES = IDX_OFF + kMlaSplit * 4;
 };
 
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
       const int h = ht * 16 + 4 * g + i;
       m[ht][i] = fmaxf(fmaxf(red[h], red[HT * 16 + h]), fmaxf(red[2 * HT * 16 + h], red[3 * HT * 16 + h]));
     }
-  __syncthreads();  // every wave has read the maxima before the sums overwrite them
+  red = reinterpret_cast<float*>(smem + S::SUM_OFF);  // the sums go to their own slots: no barrier here
   // probabilities relative to the split's max (0 where masked, and for a split with no
   // visible position), stored as bf16 P[head][key]; their fp32 sums per head
   uint16_t* P = reinterpret_cast<uint16_t*>(smem + S::P_OFF);
