@@ -72,9 +72,11 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
   // as -1; query rows h < heads, 576 bf16 each (rows past them zero), as 16-byte chunks
   constexpr int QCH = HT * 16 * 72;  // 64 chunks of q_nope + 8 of q_pe per head
   constexpr int QPT = (QCH + kMlaThreads - 1) / kMlaThreads;
+  // every wave loads all 64 positions (lane l: row l) and hands them out by readlane / lane
+  // shuffle, so the gather needs no barrier
   int t_idx = -1;
   {
-    const int j = split * kMlaSplit + min(tid, kMlaSplit - 1);
+    const int j = split * kMlaSplit + lane;
     t_idx = indices[static_cast<int64_t>(s) * topk + min(j, topk - 1)];
     if (j >= topk || t_idx < 0 || t_idx >= T || (seqlen > 1 && t_idx > *cur_pos + s)) t_idx = -1;
   }
@@ -86,24 +88,24 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     qv[u] = k < 64 ? reinterpret_cast<const u32x4s*>(q_nope + (static_cast<int64_t>(s) * heads + h) * kMlaDim)[k]
                    : reinterpret_cast<const u32x4s*>(q_pe + (static_cast<int64_t>(s) * heads + h) * kMlaPe)[k - 64];
   }
-  if (tid < kMlaSplit) idx_l[tid] = t_idx;
-  __syncthreads();  // the positions (the queries go to LDS once the gather is in flight)
+  if (tid < kMlaSplit) idx_l[tid] = t_idx;  // read after the gather's barrier
   // gather: kv row of position idx_l[row] into LDS row `row` (64 chunks of 16 B), pe row
   // (8 chunks); a masked row is loaded from row 0 (unconditional loads) and stored as
   // zeros, so whatever row 0 holds cannot reach the products
   {
+    // kv: chunk tid + 256 u is row wave + 4 u (wave-uniform), chunk lane; pe: row
+    // (tid >> 3) + 32 u, chunk tid & 7
     u32x4s v[16], w[2];
+    int tv[16], tw[2];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int c = tid + u * kMlaThreads, row = c >> 6, ch = c & 63;
-      const int t = max(idx_l[row], 0);
-      v[u] = reinterpret_cast<const u32x4s*>(kv + static_cast<int64_t>(t) * kMlaDim)[ch];
+      tv[u] = __builtin_amdgcn_readlane(t_idx, wave + 4 * u);
+      v[u] = reinterpret_cast<const u32x4s*>(kv + static_cast<int64_t>(max(tv[u], 0)) * kMlaDim)[lane];
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + u * kMlaThreads, row = c >> 3, ch = c & 7;
-      const int t = max(idx_l[row], 0);
-      w[u] = reinterpret_cast<const u32x4s*>(pe + static_cast<int64_t>(t) * kMlaPe)[ch];
+      tw[u] = __shfl(t_idx, ((tid >> 3) + 32 * u) & 63);
+      w[u] = reinterpret_cast<const u32x4s*>(pe + static_cast<int64_t>(max(tw[u], 0)) * kMlaPe)[tid & 7];
     }
     const u32x4s zero = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -116,13 +118,13 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
     }
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const int c = tid + u * kMlaThreads, row = c >> 6, ch = c & 63;
-      *reinterpret_cast<u32x4s*>(smem + S::KV_OFF + row * kMlaKvStride + ch * 16) = idx_l[row] >= 0 ? v[u] : zero;
+      const int row = wave + 4 * u;
+      *reinterpret_cast<u32x4s*>(smem + S::KV_OFF + row * kMlaKvStride + lane * 16) = tv[u] >= 0 ? v[u] : zero;
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int c = tid + u * kMlaThreads, row = c >> 3, ch = c & 7;
-      *reinterpret_cast<u32x4s*>(smem + S::PE_OFF + row * kMlaPe * 2 + ch * 16) = idx_l[row] >= 0 ? w[u] : zero;
+      const int row = (tid >> 3) + 32 * u;
+      *reinterpret_cast<u32x4s*>(smem + S::PE_OFF + row * kMlaPe * 2 + (tid & 7) * 16) = tw[u] >= 0 ? w[u] : zero;
     }
   }
   __syncthreads();
