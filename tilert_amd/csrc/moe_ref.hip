@@ -227,24 +227,16 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
 #pragma unroll
   for (int i = 0; i < 4; ++i) ck[i] = live[i] ? route_key(b[i]) : 0u;
   int my_e = 0;
-  float my_s = 0.f, sum = 0.f;
   auto round = [&](int r) __attribute__((always_inline)) {
     const uint32_t best = wave_max_u32(max(max(ck[0], ck[1]), max(ck[2], ck[3])));
     const uint64_t b0 = __ballot(ck[0] == best), b1 = __ballot(ck[1] == best), b2 = __ballot(ck[2] == best),
                    b3 = __ballot(ck[3] == best);
     const int col = b0 ? 0 : (b1 ? 1 : (b2 ? 2 : 3));
     const int owner = __builtin_ctzll(b0 ? b0 : (b1 ? b1 : (b2 ? b2 : b3)));
-    const int be = 64 * col + owner;
-    const float sc = col == 0 ? s[0] : (col == 1 ? s[1] : (col == 2 ? s[2] : s[3]));  // uniform select
-    const float sv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, sc), owner));
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (i == col && lane == owner) ck[i] = 0u;
-    if (lane == r) {
-      my_e = be;
-      my_s = sv;
-    }
-    sum += sv;
+    if (lane == r) my_e = 64 * col + owner;
   };
   if (topk == 8) {  // both models' k: the rounds unrolled
 #pragma unroll
@@ -252,6 +244,13 @@ __device__ inline void route_one(const float* __restrict__ srow, const float* __
   } else {
     for (int r = 0; r < topk; ++r) round(r);
   }
+  // lane r < topk: the unbiased score of its expert, from the lane that holds it; their sum
+  // in round order
+  const int own = my_e & 63, colr = my_e >> 6;
+  const float s0 = __shfl(s[0], own), s1 = __shfl(s[1], own), s2 = __shfl(s[2], own), s3 = __shfl(s[3], own);
+  const float my_s = colr == 0 ? s0 : (colr == 1 ? s1 : (colr == 2 ? s2 : s3));
+  float sum = 0.f;
+  for (int r = 0; r < topk; ++r) sum += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_s), r));
   out_e = my_e;
   out_p = my_s / sum * route_scale;
 }
