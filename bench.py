@@ -611,7 +611,8 @@ def bench_m_sweep(torch, dev, cpu=True):
 
 def extras(torch, dev):
     """Launch-latency-sized ops of the path, beyond the configurations: RMSNorm + act_quant,
-    the paged indexer, the indexer key producer and sparse MLA attention."""
+    the paged indexer, the indexer key producer, the indexer's input projections and sparse
+    MLA attention."""
     from tilert_amd import sparse_index as si
     from tilert_amd.rmsnorm import rmsnorm_quant
     out = {}
@@ -659,6 +660,37 @@ def extras(torch, dev):
     us_2 = _graph_time_us(torch, two_step, st, 5)
     out["ki_producer_M4"] = {"fused_us": round(us_f, 2), "bf16_cache_then_page_write_us": round(us_2, 2)}
     del kpages, kcache
+
+    # the indexer's input projections at decode (M = 4, DeepSeek-V3.2): projx_wqaki (wq_a
+    # and the indexer's wk in one FP8 GEMV, 1536 + 128 rows), projx_wis (the bf16 64 x 7168
+    # weights_proj GEMV) and the DECOUPLED RMSNormProjxWqakis (rmsnorm_quant + the two),
+    # 8 rotating weight sets
+    from tilert_amd.projx_wqaki import pack_wqaki, projx_wis, projx_wqaki, rmsnorm_projx_wqakis
+    gi = torch.Generator().manual_seed(31)
+    pk, wis = [], []
+    for _ in range(8):
+        wq_, wqs_ = K_.weight_quant(randn(torch, (1536, 7168), gi, dev, 0.02))
+        wk_, wks_ = K_.weight_quant(randn(torch, (128, 7168), gi, dev, 0.02))
+        pk.append(pack_wqaki(wq_, wqs_, wk_, wks_))
+        wis.append(randn(torch, (64, 7168), gi, dev, 0.02).to(torch.bfloat16))
+    xi = [randn(torch, (1, M, 7168), gi, dev).to(torch.bfloat16) for _ in range(4)]
+    xiq, xis = K_.act_quant(xi[0])
+    gi_ = (torch.rand(7168, generator=gi) * 0.2 + 0.9).to(dev)
+    qi = torch.empty(1, M, 1536, dtype=torch.bfloat16, device=dev)
+    kii = torch.empty(1, M, 128, dtype=torch.bfloat16, device=dev)
+    sci = torch.empty(1, M, 64, dtype=torch.bfloat16, device=dev)
+    us_a = _graph_time_us(torch, lambda i: projx_wqaki(xiq, xis, pk[i % 8], qi, kii, None,
+                                                       model_arch="deepseek_v3_2"), st, 5)
+    us_w = _graph_time_us(torch, lambda i: projx_wis(xi[i % 4], wis[i % 8], sci), st, 5)
+    us_r = _graph_time_us(torch, lambda i: rmsnorm_projx_wqakis(xi[i % 4], gi_, pk[i % 8], wis[i % 8], qi, kii, sci,
+                                                                model_arch="deepseek_v3_2"), st, 5)
+    b_a = gemm_bytes(M, 1664, 7168)
+    b_w = 64 * 7168 * 2 + M * 7168 * 2 + M * 64 * 2
+    out["indexer_projections_M4"] = {
+        "projx_wqaki": {"us": round(us_a, 2), "GBs": round(b_a / us_a / 1e3, 1)},
+        "projx_wis": {"us": round(us_w, 2), "GBs": round(b_w / us_w / 1e3, 1)},
+        "rmsnorm_projx_wqakis": {"us": round(us_r, 2), "launches": 3}}
+    del pk, wis
 
     # sparse MLA decode attention over the top-2048 of a 128K latent cache: 4 tokens x 16
     # heads (TP=8 share), independent selections per token, 3 rotating caches (> MALL)

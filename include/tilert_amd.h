@@ -286,9 +286,13 @@ int tl_projx_wqaki(const void* x_q, const float* x_s, const void* w_packed, cons
 /* y bf16 [M, N] = bf16(x . w^T) with bf16 x [M, K] and bf16 weights w [N, K] (row-major),
  * fp32 accumulation: proj_w_op, the indexer head-weight projection of projx_wis
  * (deepseek_v3_2/ops/projx_wis.py:18-37; golden RMSNormProjxWqakis :289-299).  M <= 16,
- * N % 16 == 0, K % 128 == 0, K <= 8192. */
+ * N % 16 == 0 (N <= 262144), K % 128 == 0 (K <= 65536).  K is split over workgroups: the
+ * workspace (tl_bf16_gemv_workspace_bytes; 0 bytes when K <= 512) is the zero-initialised
+ * split-K workspace of tl_fp8_gemm -- its counter region is left zero by every call, so
+ * one buffer per stream serves both. */
+size_t tl_bf16_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int tl_bf16_gemv(const void* x_bf16, const void* w_bf16, int64_t M, int64_t N, int64_t K, void* y_bf16,
-                 void* stream);
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* RMSNorm with optional activation quantisation (rmsnorm_quant_op / rmsnorm_op,
  * ops/rmsnorm_quant.py:19-63; norm of tilert/models/common.py:92-133 without residual).

@@ -93,3 +93,20 @@ def test_rmsnorm_projq_wqi_vs_oracle(cuda, arch, q_rank, s):
     rmsnorm_projq_wqi_op(q.to(cuda), packed, None, gamma.to(cuda), iq, None, "fp16mma", arch)
     eps = 1e-6 if arch == "deepseek_v3_2" else 1e-5
     assert_gemm_close(iq[0], ref.rmsnorm_projq_wqi(q[0], gamma, wq, ws, 64, 128, eps), f"iq {arch} s={s}")
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 64, 384),     # one K slice: no workspace
+                                   (3, 32, 640),     # a last slice with one live block of four
+                                   (16, 64, 7168),   # the largest M at the production width
+                                   (1, 160, 2048)])
+def test_bf16_gemv_slices_vs_oracle(cuda, M, N, K):
+    """projx_wis's bf16 GEMV over K slices (fixed-order sum of the slices' partials),
+    twice in a row on one stream (the arrival counters are left zero for the next call)."""
+    g = synth.gen(M * 7 + N + K)
+    x = synth.activations(M, K, g)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    want = ref.projx_wis(x, w)
+    for _ in range(2):
+        y = torch.empty(1, M, N, dtype=torch.bfloat16, device=cuda)
+        projx_wis(x.reshape(1, M, K).to(cuda), w.to(cuda), y)
+        assert_gemm_close(y[0], want, f"bf16_gemv M={M} N={N} K={K}")

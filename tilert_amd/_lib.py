@@ -57,7 +57,8 @@ SIGNATURES: dict[str, tuple] = {
                                  _c_void_p]),
     "tl_projx_wqaki": (_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                               _i64, _c_void_p, _size, _c_void_p]),
-    "tl_bf16_gemv": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p]),
+    "tl_bf16_gemv": (_int, [_c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _size, _c_void_p]),
+    "tl_bf16_gemv_workspace_bytes": (_size, [_i64, _i64, _i64]),
     "tl_rmsnorm_quant": (_int, [_c_void_p, _c_void_p, ctypes.c_float, _i64, _i64, _c_void_p, _c_void_p,
                                 _c_void_p, _int, _c_void_p]),
     "tl_indexer_fp8_scores": (_int, [_c_void_p, _c_void_p, _int, _c_void_p, _c_void_p,

@@ -290,4 +290,9 @@ __device__ inline void ring_pipeline(int n, Buf (&buf)[D], Fetch&& fetch, Comput
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The split-K workspace that the FP8 GEMM and the bf16 GEMV share (one per stream): per-row-
+// tile arrival counters first, which every call leaves zero, then the fp32 partials.
+constexpr int kWsCounterTiles = 16384;  // N <= 262144
+constexpr size_t kWsCounterBytes = kWsCounterTiles * sizeof(uint32_t);
+
 }  // namespace tl

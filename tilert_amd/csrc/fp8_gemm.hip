@@ -1015,8 +1015,8 @@ static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, bool packed) {
 // The workspace starts with a fixed counter region (one uint32 per 16-row tile, for
 // every problem size) that stays all-zero between calls; fp32 partials follow it.  A
 // fixed region keeps one problem's partials from ever landing on another's counters.
-constexpr int kMaxRowTiles = 16384;  // N <= 262144
-constexpr size_t kCounterBytes = kMaxRowTiles * sizeof(uint32_t);
+constexpr int kMaxRowTiles = kWsCounterTiles;  // N <= 262144
+constexpr size_t kCounterBytes = kWsCounterBytes;
 
 // Workspace: counters, then the split-K partials, then the activation image (256-aligned).
 

@@ -97,7 +97,13 @@ def projx_wis(x_in: torch.Tensor, w: torch.Tensor, output: torch.Tensor, compute
     if output.dtype != torch.bfloat16 or output.numel() != M * N or not output.is_contiguous():
         raise ValueError(f"projx_wis: output must be a contiguous bfloat16 [1, s, {N}] tensor")
     _require_cuda("projx_wis", x_in, w, output)
-    _lib.call("tl_bf16_gemv", x_in.data_ptr(), w.data_ptr(), M, N, dim, output.data_ptr(), _stream(x_in))
+    st = _stream(x_in)
+    nbytes = _lib.query("tl_bf16_gemv_workspace_bytes", M, N, dim)
+    ws_ptr, ws_len = None, 0
+    if nbytes:
+        ws = _WS.get(x_in.device, st, nbytes)
+        ws_ptr, ws_len = ws.data_ptr(), ws.numel()
+    _lib.call("tl_bf16_gemv", x_in.data_ptr(), w.data_ptr(), M, N, dim, output.data_ptr(), ws_ptr, ws_len, st)
 
 
 _NO_LOGS: dict = {}
