@@ -121,13 +121,13 @@ __global__ __launch_bounds__(kHgMaxWaves * 64, 2) void head_gemm_kernel(
 // accumulation on v_mfma_f32_16x16x32_bf16: proj_w_op, the indexer's head-weight projection
 // (deepseek_v3_2/ops/projx_wis.py:18-37; its weights_proj stays bf16, rmsnorm_projx_wqakis.py:38-41).
 // The weight is narrow (64 x 7168: four 16-row tiles), so K is split: workgroup (tile, s)
-// of 4 waves takes K blocks 4 s .. 4 s + 3 (one per wave, all loads issued before the
+// of 8 waves takes K blocks 8 s .. 8 s + 7 (one per wave, all loads issued before the
 // MFMAs), its waves are reduced through LDS in wave order, and with more than one slice
 // the fp32 tile partials go to the workspace; the tile's last slice to arrive (an
 // agent-scope counter, left zero again) adds them in slice order and writes y, so the
-// result is deterministic.  At 64 x 7168, M = 4: 8.1 us, against 12.2 us for one 16-wave
-// workgroup per tile (four CUs streaming the whole weight).
-constexpr int kBgWaves = 4;  // K blocks per slice, one per wave
+// result is deterministic.  At 64 x 7168, M = 4: 6.9 us (slices of 4 / 16 blocks: 8.1 /
+// 7.2 us), against 12.2 us for one 16-wave workgroup per tile (four CUs streaming it all).
+constexpr int kBgWaves = 8;  // K blocks per slice, one per wave
 
 __global__ __launch_bounds__(kBgWaves * 64) void bf16_gemv_kernel(const uint16_t* __restrict__ x,
                                                                   const uint16_t* __restrict__ w, int M, int N, int K,
