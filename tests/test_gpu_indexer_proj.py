@@ -96,7 +96,7 @@ def test_rmsnorm_projq_wqi_vs_oracle(cuda, arch, q_rank, s):
 
 
 @pytest.mark.parametrize("M,N,K", [(4, 64, 384),     # one K slice: no workspace
-                                   (3, 32, 640),     # a last slice with one live block of four
+                                   (3, 32, 1152),    # a last slice with one live block of eight
                                    (16, 64, 7168),   # the largest M at the production width
                                    (1, 160, 2048)])
 def test_bf16_gemv_slices_vs_oracle(cuda, M, N, K):
