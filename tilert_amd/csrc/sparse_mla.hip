@@ -248,40 +248,44 @@ __global__ __launch_bounds__(kMlaThreads) void sparse_mla_split_kernel(
   (void)n_splits;
 }
 
-// One 64-thread workgroup per (head, token, quarter of the 512 dims): 2 dims per thread;
-// the 32 split rows are loaded together (unconditional, clamped; splits past n_splits
-// weigh 0).  The split weights are computed lane-parallel (lane j: split j's lse, its
-// exponentials; max and sum by DPP) and read back per split with readlane: every lane
-// would otherwise evaluate all 64 exponentials, and this one-wave kernel is issue-bound.
+// One 64-thread workgroup per (head, token, quarter of the 512 dims).  Lane l takes dims
+// 4 (l % 32) .. +3 of the quarter and the splits of parity l / 32 (16-byte loads, 16 per
+// lane, unconditional and clamped; splits past n_splits weigh 0); the two half-waves' sums
+// meet through a lane shuffle and each half stores two of the four dims.  The split lse is
+// requested first (memory operations complete in order, so the weights are computed while
+// the split rows arrive); the weights are computed lane-parallel (lane j: split j's lse,
+// its exponentials; max and sum by DPP) and read back per split with readlane.
 __global__ __launch_bounds__(64) void sparse_mla_combine_kernel(const float* __restrict__ out_acc,
                                                                 const float* __restrict__ lse_acc, int heads,
                                                                 int n_splits, uint16_t* __restrict__ out,
                                                                 float* __restrict__ lse) {
   const int h = blockIdx.x, s = blockIdx.y, quarter = blockIdx.z, tid = threadIdx.x;
   const int64_t row = static_cast<int64_t>(s) * heads + h;
-  const int d0 = quarter * 128 + 2 * tid;
-  // the split lse first: memory operations complete in order, so the weights below are
-  // computed while the split rows are still arriving
+  const int d0 = quarter * 128 + 4 * (tid & 31), par = tid >> 5;
+  constexpr int kHalf = kMlaMaxSplits / 2;
   const float lj = tid < n_splits ? lse_acc[row * kMlaMaxSplits + min(tid, kMlaMaxSplits - 1)] : -INFINITY;
   __builtin_amdgcn_sched_barrier(0);
-  float2 v[kMlaMaxSplits];
+  v4f v[kHalf];
 #pragma unroll
-  for (int j = 0; j < kMlaMaxSplits; ++j)
-    v[j] = *reinterpret_cast<const float2*>(out_acc + (row * kMlaMaxSplits + min(j, n_splits - 1)) * kMlaDim + d0);
+  for (int i = 0; i < kHalf; ++i)
+    v[i] = *reinterpret_cast<const v4f*>(out_acc + (row * kMlaMaxSplits + min(2 * i + par, n_splits - 1)) * kMlaDim + d0);
   __builtin_amdgcn_sched_barrier(0);
   const float mx = wave_max_f32(lj);
   const float sum = wave_sum_f32(lj == -INFINITY ? 0.f : expf(lj - mx));
   const float L = mx == -INFINITY ? -INFINITY : mx + logf(sum);
-  const float wl = lj == -INFINITY ? 0.f : expf(lj - L);  // lane j: split j's weight
-  float a0 = 0.f, a1 = 0.f;
+  const int wl = __builtin_bit_cast(int, lj == -INFINITY ? 0.f : expf(lj - L));  // lane j: split j's weight
+  v4f a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < kMlaMaxSplits; ++j) {
-    const float wj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j));
-    a0 += v[j].x * wj;
-    a1 += v[j].y * wj;
+  for (int i = 0; i < kHalf; ++i) {
+    const float we = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wl, 2 * i));
+    const float wo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(wl, 2 * i + 1));
+    a += v[i] * (par ? wo : we);
   }
-  reinterpret_cast<uint32_t*>(out + row * kMlaDim + d0)[0] =
-      f32_to_bf16(a0) | (static_cast<uint32_t>(f32_to_bf16(a1)) << 16);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) a[k] += __shfl_xor(a[k], 32);  // even + odd splits (the same sum in both halves)
+  const float lo = par ? a[2] : a[0], hi = par ? a[3] : a[1];
+  reinterpret_cast<uint32_t*>(out + row * kMlaDim + d0)[par] =
+      f32_to_bf16(lo) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
   if (quarter == 0 && tid == 0) lse[row] = L;
 }
 
